@@ -1,0 +1,96 @@
+// gfx950 (CDNA4) device primitives of the FlashAttention-2 forward. Each wraps one
+// instruction the kernel is built from; tests/blocks/fa_blocks.hip pins their lane layouts and
+// numerics on the GPU.
+//
+// Counterparts of the reference's Ampere primitives (csrc/common.cuh), not translations:
+//   cp.async 16 B (common.cuh:57-68)        -> lds_dma16: global_load_lds_dwordx4
+//   ldmatrix_x4 (common.cuh:73-79)          -> plain ds_read_b128 of a swizzled row chunk
+//   ldmatrix_x4_trans (common.cuh:80-84)    -> lds_read_tr16: ds_read_b64_tr_b16
+//   mma_16816 f32 acc (common.cuh:91-98)    -> mfma32: v_mfma_f32_32x32x16_f16
+//   __shfl_xor row reductions (flash_fwd.cu:359-363, 535-537)
+//                                           -> max_xor32 / sum_xor32: v_permlane32_swap
+//   exp2f / ex2.approx (common.cuh:124-128) -> exp2_fast: v_exp_f32
+//   pack_half2 RN (common.cuh:113-117)      -> pack8: v_cvt_pk_f16_f32 (round to nearest even)
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace fa::dev {
+
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+#define FA_LDS __attribute__((address_space(3)))
+
+// D(32x32, fp32) += A(32x16, fp16) * B(16x32, fp16); 32 cycles per wave on one SIMD.
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// D(16x16, fp32) += A(16x32, fp16) * B(32x16, fp16).
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Transposing LDS read: see fa::geom::tr16_row / tr16_col for the addressing.
+__device__ __forceinline__ f16x4 lds_read_tr16(const char* lds_generic) {
+    const fp16x4_t FA_LDS* p = (const fp16x4_t FA_LDS*)(lds_generic);
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                                         const_cast<fp16x4_t FA_LDS*>(p)));
+}
+
+// 16-byte global -> LDS copy that bypasses VGPRs. Lane i of the wave writes its 16 bytes to
+// lds_wave_base + 16*i; lds_wave_base must be wave-uniform. Completion is tracked by vmcnt.
+__device__ __forceinline__ void lds_dma16(const void* global_src, char* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(global_src, (void FA_LDS*)(lds_wave_base), 16, 0, 0);
+}
+
+// Wait until every global load of this wave (including LDS DMA) has landed.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Combine a per-lane value with the one held by lane ^ 32 (the other half of the wave). The
+// swap yields the pair {x[l], x[l^32]} in every lane, so max and sum need no lane select.
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Eight fp32 values -> eight fp16 (RNE), as one MFMA operand.
+__device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, float a4,
+                                       float a5, float a6, float a7) {
+    const f16x2 p0 = __builtin_convertvector(f32x2{a0, a1}, f16x2);
+    const f16x2 p1 = __builtin_convertvector(f32x2{a2, a3}, f16x2);
+    const f16x2 p2 = __builtin_convertvector(f32x2{a4, a5}, f16x2);
+    const f16x2 p3 = __builtin_convertvector(f32x2{a6, a7}, f16x2);
+    return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+__device__ __forceinline__ f16x4 pack4(float a0, float a1, float a2, float a3) {
+    const f16x2 p0 = __builtin_convertvector(f32x2{a0, a1}, f16x2);
+    const f16x2 p1 = __builtin_convertvector(f32x2{a2, a3}, f16x2);
+    return f16x4{p0[0], p0[1], p1[0], p1[1]};
+}
+
+__device__ __forceinline__ bool wave_any(bool pred) {
+    return __builtin_amdgcn_ballot_w64(pred) != 0;
+}
+
+__device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+}  // namespace fa::dev

@@ -1,0 +1,102 @@
+// Integer tile geometry of the gfx950 FlashAttention-2 forward: LDS swizzle, MFMA register
+// layouts, transpose-read addressing, tile counts and the workgroup -> (head, query block) map.
+//
+// Plain constexpr C++ with no HIP types: clang compiles constexpr functions for both host and
+// device, so the kernel and the host-side unit tests (built with g++) use this one definition.
+#pragma once
+
+#include <cstdint>
+
+namespace fa::geom {
+
+// ---- LDS layout of a K or V tile ------------------------------------------------------------
+// A tile is [rows][D] fp16, row-major, 2*D bytes per row (128 B for D=64, 256 B for D=128), so
+// every row starts on the same LDS bank. The 16-byte chunks of a row are permuted by an XOR
+// with a 3-bit function of the row, which breaks the two conflicting access patterns:
+//   * K fragments (ds_read_b128): 8 consecutive lanes read the same logical chunk of 8
+//     consecutive rows; row_xor(row & 7) takes 8 distinct values, so those lanes hit 8
+//     distinct 16-byte bank groups (all 32 banks of a 128-byte LDS cycle).
+//   * V fragments (ds_read_b64_tr_b16): a 16-lane group reads chunks {c, c+1} (c even) of 4
+//     consecutive rows starting at a multiple of 4; row_xor of those rows is {0,2,4,6} + b,
+//     so the 8 chunks read are distinct.
+// Replaces the reference's 8-row XOR swizzle for ldmatrix (csrc/common.cuh:38-42), which is
+// matched to a different access pattern (8-row ldmatrix phases, no transpose reads).
+constexpr int row_xor(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+
+// Physical chunk slot of logical 16-byte chunk `chunk` of `row`. For a fixed row this is an
+// involution (XOR), so the same function maps physical slots back to logical chunks.
+constexpr int swizzle_chunk(int row, int chunk) { return chunk ^ row_xor(row); }
+
+// Byte offset of (row, logical chunk) inside a tile with `row_bytes` bytes per row.
+constexpr int tile_offset(int row, int chunk, int row_bytes) {
+    return row * row_bytes + 16 * swizzle_chunk(row, chunk);
+}
+
+// ---- v_mfma_f32_32x32x16_f16 register layouts (wave64) --------------------------------------
+// A (32x16): lane l holds A[l % 32][8*(l/32) + i], i = 0..7.
+// B (16x32): lane l holds B[8*(l/32) + i][l % 32], i = 0..7.
+// C (32x32): lane l, accumulator r (0..15) holds C[mfma32_c_row(l, r)][l % 32].
+// Only the C mapping and the m/n indices matter for correctness: the k index of A and B is
+// paired lane-by-lane, so any consistent k order gives the same product.
+constexpr int mfma32_c_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+constexpr int mfma32_c_col(int lane) { return lane & 31; }
+
+// v_mfma_f32_16x16x32_f16: A (16x32) lane l holds A[l % 16][8*(l/16) + i]; B likewise;
+// C (16x16): lane l, accumulator r (0..3) holds C[4*(l/16) + r][l % 16].
+constexpr int mfma16_c_row(int lane, int r) { return 4 * (lane >> 4) + r; }
+constexpr int mfma16_c_col(int lane) { return lane & 15; }
+
+// ---- Transposed operand reads (ds_read_b64_tr_b16) ------------------------------------------
+// Within each group of 16 lanes, the instruction loads a 4 x 16 block of 16-bit values
+// (4 rows, 16 consecutive columns) and returns it transposed: lane j of the group receives
+// column j, rows 0..3, as its four halves. tr16_row / tr16_col give the (row, column) that
+// lane j must address (8 bytes = 4 columns starting there) for that result.
+constexpr int tr16_row(int lane) { return (lane & 15) >> 2; }
+constexpr int tr16_col(int lane) { return 4 * (lane & 3); }
+
+// ---- Score-tile index maps (S^T = K Q^T in 32x32 MFMA blocks) --------------------------------
+// Key offset within a tile of accumulator r of 32-key block nb held by `lane`; that lane's
+// query is always lane % 32 of the wave's 32 queries.
+constexpr int st_key(int lane, int nb, int r) { return 32 * nb + mfma32_c_row(lane, r); }
+
+// Key offset (within a 16-key MFMA step) of operand slot i (0..7) of the P.V product. Equal to
+// the score accumulator that feeds it: slot i of step h is accumulator 8*h + i of its block.
+constexpr int pv_key(int lane, int i) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
+
+// ---- Work decomposition ---------------------------------------------------------------------
+constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Number of K/V tiles a workgroup whose first query row is q0 visits. Causal workgroups stop
+// at the tile holding their last query's diagonal (tiles above it are fully masked);
+// follows csrc/kernels/flash_fwd.cu:193-194 (kv_end = min(n, q0 + BR)).
+constexpr int num_kv_tiles(int n, int q0, int block_q, int block_k, bool causal) {
+    const int kv_end = causal ? (n < q0 + block_q ? n : q0 + block_q) : n;
+    return ceil_div(kv_end, block_k);
+}
+
+// Whether a tile [kt, kt+block_k) needs any masking for queries [qw, qw+rows): keys past the
+// end of the sequence, or (causal) keys right of the diagonal of the first query.
+// Follows the needs_mask test of csrc/kernels/flash_fwd.cu:502-505.
+constexpr bool tile_needs_mask(int n, int kt, int block_k, int qw, bool causal) {
+    return (kt + block_k > n) || (causal && kt + block_k - 1 > qw);
+}
+
+// Whether every key of the tile is masked for all queries [qw, qw+rows) (causal only).
+constexpr bool tile_fully_masked(int kt, int qw, int rows, bool causal) {
+    return causal && kt > qw + rows - 1;
+}
+
+// Workgroup id -> (batch*head index, query block). Consecutive ids share the query block and
+// walk the heads; the hardware deals consecutive ids round-robin to the 8 XCDs, so each XCD
+// keeps a fixed subset of heads (whose K/V then stay in that XCD's L2) when B*H is a multiple
+// of 8. Causal runs the longest query blocks first (as csrc/kernels/flash_fwd.cu:183-185).
+struct Work {
+    int bh;
+    int qb;
+};
+constexpr Work work_of(int block_id, int bh_count, int n_qblocks, bool causal) {
+    const int qi = block_id / bh_count;
+    return Work{block_id % bh_count, causal ? n_qblocks - 1 - qi : qi};
+}
+
+}  // namespace fa::geom

@@ -1,0 +1,12 @@
+# Type stub for the compiled extension (csrc/bindings.cpp), as the reference's fa/_C.pyi.
+import torch
+
+def forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    softmax_scale: float | None = None,
+    variant: str = "opt",
+) -> torch.Tensor: ...
+def version() -> str: ...

@@ -1,0 +1,97 @@
+"""ctypes view of the C ABI in include/fa_hip.h (libfa_hip.so next to this file).
+
+Used by the tests and the benchmark to call the launcher without PyTorch types in between,
+and by any caller that wants the raw entry points. Loading the library touches no GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libfa_hip.so"
+
+FA_OK, FA_EINVAL, FA_EHIP = 0, 1, 2
+VARIANTS = {"baseline": 0, "opt": 1, "fp16acc": 2}
+
+
+class FaParams(ctypes.Structure):
+    """struct fa_params (include/fa_hip.h)."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("seqlen", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("causal", ctypes.c_uint8),
+        ("variant", ctypes.c_uint8),
+        ("reserved", ctypes.c_uint8 * 2),
+    ]
+
+
+class FaTileInfo(ctypes.Structure):
+    """struct fa_tile_info (include/fa_hip.h)."""
+
+    _fields_ = [
+        ("block_q", ctypes.c_int32),
+        ("block_k", ctypes.c_int32),
+        ("waves", ctypes.c_int32),
+        ("lds_bytes", ctypes.c_int32),
+    ]
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(f"fa: {LIB_PATH} is not built (run flash-attention-from-scratch_amd/fa_build.py)")
+    so = ctypes.CDLL(str(LIB_PATH))
+    so.fa_flash_fwd.argtypes = [ctypes.POINTER(FaParams), ctypes.c_void_p]
+    so.fa_flash_fwd.restype = ctypes.c_int
+    so.fa_last_error.argtypes = []
+    so.fa_last_error.restype = ctypes.c_char_p
+    so.fa_tile_config.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                  ctypes.POINTER(FaTileInfo)]
+    so.fa_tile_config.restype = ctypes.c_int
+    so.fa_version.argtypes = []
+    so.fa_version.restype = ctypes.c_char_p
+    return so
+
+
+def make_params(q: int, k: int, v: int, o: int, batch: int, heads: int, seqlen: int,
+                head_dim: int, softmax_scale: float, causal: bool, variant: str | int = "opt"
+                ) -> FaParams:
+    p = FaParams()
+    p.q, p.k, p.v, p.o = q, k, v, o
+    p.batch, p.heads, p.seqlen, p.head_dim = batch, heads, seqlen, head_dim
+    p.softmax_scale = softmax_scale
+    p.causal = 1 if causal else 0
+    p.variant = VARIANTS[variant] if isinstance(variant, str) else int(variant)
+    return p
+
+
+def flash_fwd(params: FaParams, stream: int | None = None) -> tuple[int, str]:
+    """Calls fa_flash_fwd; returns (status, fa_last_error())."""
+    so = lib()
+    rc = so.fa_flash_fwd(ctypes.byref(params), ctypes.c_void_p(stream or 0))
+    return rc, so.fa_last_error().decode()
+
+
+def tile_config(head_dim: int, causal: bool, variant: str | int = "opt") -> dict:
+    so = lib()
+    info = FaTileInfo()
+    var = VARIANTS[variant] if isinstance(variant, str) else int(variant)
+    rc = so.fa_tile_config(head_dim, 1 if causal else 0, var, ctypes.byref(info))
+    if rc != FA_OK:
+        raise ValueError(so.fa_last_error().decode())
+    return {"block_q": info.block_q, "block_k": info.block_k, "waves": info.waves,
+            "lds_bytes": info.lds_bytes}
+
+
+def version() -> str:
+    return lib().fa_version().decode()

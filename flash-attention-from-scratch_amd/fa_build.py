@@ -1,0 +1,146 @@
+"""Builds the native parts in-tree, for gfx950 only.
+
+    python flash-attention-from-scratch_amd/fa_build.py            # everything
+    python flash-attention-from-scratch_amd/fa_build.py --only lib # one target
+
+Targets (outputs are git-ignored; they travel to the GPU box with the source tree):
+  lib     fa/libfa_hip.so        HIP kernels + the C ABI of include/fa_hip.h (hipcc, gfx950)
+  ext     fa/_C.<abi>.so         PyTorch-ROCm binding (g++ against torch's headers), links lib
+  blocks  tests/blocks/libfa_blocks.so   building-block kernels for the GPU unit tests
+  oracle  oracle/liboracle_fp64.so       the C fp64 oracle (gcc), test infrastructure only
+  geom    tests/geometry/libfa_geom.so   host build of the tile geometry, for the CPU tests
+
+Counterpart of the reference's setup.py / CMakeLists.txt / Makefile build targets
+(setup.py:12-33, CMakeLists.txt:56-87, Makefile:21-32): the kernel library is compiled by
+hipcc directly (no CUDAExtension, no hipify) and the binding is a plain C++ extension.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shlex
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = REPO / "include"
+FA = PKG / "fa"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+
+# Every HIP compile: gfx950 only, and no packed-fp32 VALU instructions (v_pk_fma_f32 and
+# friends), which this fleet has seen give silently wrong results.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def _run(cmd: list[str], quiet: bool = False) -> None:
+    if not quiet:
+        print("+", " ".join(shlex.quote(c) for c in cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: drop that noise.
+    err = "\n".join(
+        line for line in res.stderr.splitlines() if "packed-fp32-ops" not in line and line.strip()
+    )
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    if err and not quiet:
+        print(err, file=sys.stderr)
+
+
+def _hipcc() -> str:
+    return str(ROCM / "bin" / "hipcc")
+
+
+def build_lib(extra: list[str] | None = None) -> Path:
+    out = FA / "libfa_hip.so"
+    cmd = [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}",
+           str(CSRC / "flash_fwd.hip"), "-o", str(out), *(extra or [])]
+    _run(cmd)
+    return out
+
+
+def _ext_suffix() -> str:
+    return sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+
+
+def build_ext() -> Path:
+    import torch
+    from torch.utils import cpp_extension
+
+    out = FA / f"_C{_ext_suffix()}"
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [f"-I{p}" for p in cpp_extension.include_paths()]
+    pyinc = sysconfig.get_paths()["include"]
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *incs, f"-I{pyinc}", f"-I{ROCM / 'include'}", f"-I{INCLUDE}",
+        str(CSRC / "bindings.cpp"),
+        f"-L{FA}", "-lfa_hip",
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        "-Wl,-rpath,$ORIGIN",
+        "-o", str(out),
+    ]
+    _run(cmd)
+    return out
+
+
+def build_blocks() -> Path:
+    src = REPO / "tests" / "blocks" / "fa_blocks.hip"
+    out = src.parent / "libfa_blocks.so"
+    cmd = [_hipcc(), *HIP_FLAGS, "-shared", f"-I{CSRC}", str(src), "-o", str(out)]
+    _run(cmd)
+    return out
+
+
+def build_oracle() -> Path:
+    src = REPO / "oracle" / "attention_fp64.c"
+    out = REPO / "oracle" / "liboracle_fp64.so"
+    _run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-Wextra", str(src),
+          "-o", str(out), "-lm"])
+    return out
+
+
+def build_geom() -> Path:
+    src = REPO / "tests" / "geometry" / "geom_shim.cpp"
+    out = src.parent / "libfa_geom.so"
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{CSRC}",
+          str(src), "-o", str(out)])
+    return out
+
+
+TARGETS = {"lib": build_lib, "ext": build_ext, "blocks": build_blocks, "oracle": build_oracle,
+           "geom": build_geom}
+ALL = ("lib", "ext", "blocks", "oracle", "geom")
+
+
+def build_all() -> None:
+    for name in ALL:
+        TARGETS[name]()
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--only", choices=sorted(TARGETS), action="append")
+    args = ap.parse_args()
+    for name in args.only or ALL:
+        TARGETS[name]()
+
+
+if __name__ == "__main__":
+    main()

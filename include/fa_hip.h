@@ -1,0 +1,93 @@
+/*
+ * fa_hip.h -- C ABI of the MI355X (gfx950) FlashAttention-2 forward.
+ *
+ *   O = softmax(Q K^T * softmax_scale) V      Q, K, V, O: [B, H, N, D] fp16, contiguous
+ *
+ * Plain C: pointers, fixed-width integers and a void* stream. No PyTorch or C++ types, so the
+ * library can be bound from ctypes, a PyTorch extension or any C caller.
+ *
+ * Replaces, one for one, the torch-free C++ API of the reference:
+ *   fa_params          <- fa::FlashFwdParams + fa::Variant   (csrc/flash_fwd.h:12-30)
+ *   fa_flash_fwd       <- void fa::flash_fwd(const FlashFwdParams&, cudaStream_t)
+ *                                                            (csrc/flash_fwd.h:33,
+ *                                                             csrc/kernels/flash_fwd.cu:625-652)
+ *   fa_last_error      <- the what() text of the std::invalid_argument / std::runtime_error the
+ *                         reference throws (csrc/kernels/flash_fwd.cu:626-651, csrc/common.cuh:15-26)
+ * The reference signals errors with C++ exceptions; a C ABI cannot, so every entry point
+ * returns an fa_status and keeps the message in a thread-local buffer.
+ */
+#ifndef FA_HIP_H_
+#define FA_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. FA_EINVAL plays the role of std::invalid_argument, FA_EHIP of the
+ * std::runtime_error that CUDA_CHECK raises (csrc/common.cuh:15-26). */
+typedef enum fa_status {
+    FA_OK = 0,
+    FA_EINVAL = 1, /* bad argument: nothing was launched                                     */
+    FA_EHIP = 2    /* the HIP runtime refused the launch (launch-configuration error)        */
+} fa_status;
+
+/* Kernel build selector; same values as fa::Variant (csrc/flash_fwd.h:12-16).
+ * On CDNA4 the f16 MFMA always accumulates in fp32 and has no faster fp16-accumulate form,
+ * so FA_VARIANT_FP16ACC runs the same kernel as FA_VARIANT_OPT (bitwise identical output). */
+typedef enum fa_variant {
+    FA_VARIANT_BASELINE = 0, /* first correct MI355X kernel: exact rescaling, smaller tiles   */
+    FA_VARIANT_OPT = 1,      /* tuned kernel (default)                                        */
+    FA_VARIANT_FP16ACC = 2   /* accepted for API parity; identical to FA_VARIANT_OPT         */
+} fa_variant;
+
+/* Mirrors fa::FlashFwdParams (csrc/flash_fwd.h:18-30) with fixed-width fields. */
+typedef struct fa_params {
+    const void* q;         /* [B, H, N, D] fp16, contiguous, 16-byte aligned                   */
+    const void* k;         /* [B, H, N, D] fp16, contiguous, 16-byte aligned                   */
+    const void* v;         /* [B, H, N, D] fp16, contiguous, 16-byte aligned                   */
+    void* o;               /* [B, H, N, D] fp16, contiguous, 16-byte aligned (output)          */
+    int32_t batch;         /* B > 0                                                            */
+    int32_t heads;         /* H > 0                                                            */
+    int32_t seqlen;        /* N > 0, same for queries and keys                                 */
+    int32_t head_dim;      /* D: 64 or 128                                                     */
+    float softmax_scale;   /* usually 1/sqrt(D); any finite value                              */
+    uint8_t causal;        /* 0 or 1: key j is visible to query i iff j <= i                   */
+    uint8_t variant;       /* an fa_variant value                                              */
+    uint8_t reserved[2];   /* must be zero                                                     */
+} fa_params;
+
+/* Launches the forward kernel asynchronously on `stream` (a hipStream_t; NULL = the null
+ * stream) on the current HIP device and returns without synchronizing. All argument checks
+ * run before any HIP call, so FA_EINVAL never touches the device. Writes only rows < N of o.
+ * Allocates nothing; re-entrant. Faults during execution surface at the caller's next
+ * synchronization, as with any asynchronous HIP launch.
+ * Replaces fa::flash_fwd (csrc/flash_fwd.h:33; checks at csrc/kernels/flash_fwd.cu:626-651). */
+int fa_flash_fwd(const fa_params* params, void* stream);
+
+/* Message of the last failing call on this thread ("" after a success). The pointer stays
+ * valid until the next fa_* call on the same thread. */
+const char* fa_last_error(void);
+
+/* Tile geometry the launcher picks for (head_dim, causal, variant): query rows per
+ * workgroup, keys per tile, wavefronts per workgroup and LDS bytes per workgroup.
+ * Host-only, touches no device. No counterpart function in the reference, whose tiles are
+ * compile-time `using` lines (csrc/kernels/flash_fwd.cu:597-612); exported so that tests and
+ * the benchmark can report and check the grid the kernel runs. */
+typedef struct fa_tile_info {
+    int32_t block_q;       /* BR: query rows per workgroup                                     */
+    int32_t block_k;       /* BC: key rows per K/V tile                                        */
+    int32_t waves;         /* wavefronts (64 lanes) per workgroup                              */
+    int32_t lds_bytes;     /* LDS per workgroup                                                */
+} fa_tile_info;
+int fa_tile_config(int32_t head_dim, int32_t causal, int32_t variant, fa_tile_info* out);
+
+/* Library version string, e.g. "fa_hip 0.1.0 gfx950". */
+const char* fa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_HIP_H_ */

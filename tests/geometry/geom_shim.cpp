@@ -1,0 +1,33 @@
+// Host-side C wrappers around the kernel's integer tile geometry (fa_geometry.h), built with
+// g++ so the CPU tests (tests/test_geometry.py) check the very functions the kernel inlines.
+#include "fa_geometry.h"
+
+namespace g = fa::geom;
+
+extern "C" {
+int geom_row_xor(int row) { return g::row_xor(row); }
+int geom_swizzle_chunk(int row, int chunk) { return g::swizzle_chunk(row, chunk); }
+int geom_tile_offset(int row, int chunk, int row_bytes) { return g::tile_offset(row, chunk, row_bytes); }
+int geom_mfma32_c_row(int lane, int r) { return g::mfma32_c_row(lane, r); }
+int geom_mfma32_c_col(int lane) { return g::mfma32_c_col(lane); }
+int geom_mfma16_c_row(int lane, int r) { return g::mfma16_c_row(lane, r); }
+int geom_mfma16_c_col(int lane) { return g::mfma16_c_col(lane); }
+int geom_tr16_row(int lane) { return g::tr16_row(lane); }
+int geom_tr16_col(int lane) { return g::tr16_col(lane); }
+int geom_st_key(int lane, int nb, int r) { return g::st_key(lane, nb, r); }
+int geom_pv_key(int lane, int i) { return g::pv_key(lane, i); }
+int geom_num_kv_tiles(int n, int q0, int block_q, int block_k, int causal) {
+    return g::num_kv_tiles(n, q0, block_q, block_k, causal != 0);
+}
+int geom_tile_needs_mask(int n, int kt, int block_k, int qw, int causal) {
+    return g::tile_needs_mask(n, kt, block_k, qw, causal != 0) ? 1 : 0;
+}
+int geom_tile_fully_masked(int kt, int qw, int rows, int causal) {
+    return g::tile_fully_masked(kt, qw, rows, causal != 0) ? 1 : 0;
+}
+void geom_work_of(int block_id, int bh_count, int n_qblocks, int causal, int* bh, int* qb) {
+    const g::Work w = g::work_of(block_id, bh_count, n_qblocks, causal != 0);
+    *bh = w.bh;
+    *qb = w.qb;
+}
+}

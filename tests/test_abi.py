@@ -1,0 +1,132 @@
+"""CPU: the C ABI of include/fa_hip.h and the Python binding, without a GPU.
+
+* libfa_hip.so loads and exports every function the header declares;
+* the header is valid C and the ctypes struct mirrors its layout;
+* every argument check of fa_flash_fwd runs before any HIP call and returns FA_EINVAL with
+  the reference's message keywords (csrc/kernels/flash_fwd.cu:626-651,
+  tests/cpp/test_flash_fwd.cu:64-83);
+* the torch extension imports, and rejects host tensors with the reference's "CUDA" message
+  (csrc/bindings.cpp:31-33).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from fa import native
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "fa_hip.h"
+
+GOOD = dict(q=0x1000, k=0x2000, v=0x3000, o=0x4000, batch=1, heads=1, seqlen=64, head_dim=64,
+            softmax_scale=0.125, causal=False, variant="opt")
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    names = _declared_functions()
+    assert {"fa_flash_fwd", "fa_last_error", "fa_tile_config", "fa_version"} <= set(names)
+    so = native.lib()
+    for name in names:
+        assert hasattr(so, name), name
+
+
+def test_header_is_c_and_struct_layout_matches(tmp_path):
+    src = tmp_path / "abi.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "fa_hip.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu\\n\", sizeof(fa_params),"
+        " offsetof(fa_params, batch), offsetof(fa_params, softmax_scale),"
+        " offsetof(fa_params, causal), offsetof(fa_params, variant), sizeof(fa_tile_info));"
+        " return 0;}\n")
+    exe = tmp_path / "abi"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{REPO / 'include'}", str(src),
+                    "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    P = native.FaParams
+    assert got == [ctypes.sizeof(P), P.batch.offset, P.softmax_scale.offset, P.causal.offset,
+                   P.variant.offset, ctypes.sizeof(native.FaTileInfo)]
+
+
+def _call(**over):
+    args = dict(GOOD)
+    args.update(over)
+    return native.flash_fwd(native.make_params(**args))
+
+
+@pytest.mark.parametrize("over, words", [
+    (dict(batch=0), "batch, heads and seqlen must be positive"),
+    (dict(heads=-1), "batch, heads and seqlen must be positive"),
+    (dict(seqlen=0), "batch, heads and seqlen must be positive"),
+    (dict(head_dim=32), "head_dim must be 64 or 128, got 32"),
+    (dict(head_dim=96), "head_dim must be 64 or 128, got 96"),
+    (dict(variant=3), "unknown variant"),
+    (dict(q=0), "non-null"),
+    (dict(o=0), "non-null"),
+    (dict(k=0x2008), "16-byte aligned"),
+    (dict(o=0x4002), "16-byte aligned"),
+    (dict(softmax_scale=float("nan")), "finite"),
+    (dict(softmax_scale=float("inf")), "finite"),
+    (dict(seqlen=2**24, head_dim=128), "below 2^31"),
+    (dict(batch=2**20, heads=2**10, seqlen=2**10), "grid limit"),
+])
+def test_invalid_arguments_return_einval(over, words):
+    rc, msg = _call(**over)
+    assert rc == native.FA_EINVAL
+    assert words in msg
+
+
+def test_null_params_and_reserved_bytes():
+    so = native.lib()
+    assert so.fa_flash_fwd(None, None) == native.FA_EINVAL
+    assert b"NULL" in so.fa_last_error()
+    p = native.make_params(**GOOD)
+    p.reserved[0] = 1
+    assert native.flash_fwd(p)[0] == native.FA_EINVAL
+    p = native.make_params(**GOOD)
+    p.causal = 2
+    assert native.flash_fwd(p)[0] == native.FA_EINVAL
+
+
+def test_tile_config():
+    for d in (64, 128):
+        for causal in (False, True):
+            for var in ("baseline", "opt", "fp16acc"):
+                t = native.tile_config(d, causal, var)
+                assert t["block_q"] == 32 * t["waves"]
+                assert t["block_k"] % 32 == 0
+                assert t["lds_bytes"] == 4 * t["block_k"] * 2 * d
+                assert t["lds_bytes"] <= 160 * 1024
+    assert native.tile_config(64, False, "fp16acc") == native.tile_config(64, False, "opt")
+    with pytest.raises(ValueError, match="head_dim"):
+        native.tile_config(96, False)
+    with pytest.raises(ValueError, match="variant"):
+        native.tile_config(64, False, 7)
+
+
+def test_version():
+    assert "gfx950" in native.version()
+
+
+def test_extension_imports_and_rejects_host_tensors():
+    import torch
+
+    import fa
+
+    assert set(fa.__all__) >= {"forward", "forward_variant", "attention_reference"}
+    assert "gfx950" in fa._C.version()
+    q = torch.zeros(1, 1, 64, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fa.forward(q, q, q)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fa.forward_variant(q, q, q, variant="nope")

@@ -1,0 +1,156 @@
+"""CPU: the kernel's integer tile geometry (csrc/fa_geometry.h), through a g++ build of the
+same header. Counterpart of the reference's host-side swizzle checks
+(tests/cpp/test_ptx.cu:256-313: permutation and bank-conflict freedom), re-targeted to the
+gfx950 access patterns, plus the tile-count, mask and work-map arithmetic
+(csrc/kernels/flash_fwd.cu:183-194, 502-505).
+
+LDS bank model used here: 32 banks of 4 bytes (bank = byte_offset / 4 mod 32); a
+ds_read_b128 serves 8 lanes (128 bytes) per cycle and a ds_read_b64_tr_b16 one 16-lane group
+per cycle. An access group is conflict-free when it touches each bank exactly once.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import itertools
+from pathlib import Path
+
+import pytest
+
+LIB = Path(__file__).resolve().parent / "geometry" / "libfa_geom.so"
+
+
+@pytest.fixture(scope="module")
+def geo():
+    so = ctypes.CDLL(str(LIB))
+    so.geom_work_of.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
+    return so
+
+
+def _banks(byte_off, nbytes):
+    return [((byte_off + 4 * w) // 4) % 32 for w in range(nbytes // 4)]
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_swizzle_is_a_permutation_of_each_row(geo, d):
+    cpr = d // 8
+    for row in range(256):
+        phys = [geo.geom_swizzle_chunk(row, c) for c in range(cpr)]
+        assert sorted(phys) == list(range(cpr))
+        assert all(geo.geom_swizzle_chunk(row, p) == c for c, p in enumerate(phys))  # involution
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_k_fragment_reads_are_conflict_free(geo, d):
+    """ds_read_b128 of the S^T A operand: lane l reads row 32*nb + l%32, chunk 2*kk + l//32."""
+    rb = 2 * d
+    for nb, kk in itertools.product(range(2), range(d // 16)):
+        offs = [geo.geom_tile_offset(32 * nb + (l % 32), 2 * kk + l // 32, rb) for l in range(64)]
+        for g0 in range(0, 64, 8):
+            banks = sum((_banks(o, 16) for o in offs[g0:g0 + 8]), [])
+            assert sorted(banks) == list(range(32)), (nb, kk, g0)
+
+
+def _v_read_offsets(geo, d, nb, h, db, e):
+    """Byte offsets the kernel's V^T transposed reads use (flash_fwd.hip, O^T += V^T P^T)."""
+    rb = 2 * d
+    out = []
+    for l in range(64):
+        hi = l >> 5
+        row = 32 * nb + 16 * h + 8 * e + 4 * hi + geo.geom_tr16_row(l)
+        colh = 32 * db + 16 * ((l >> 4) & 1) + geo.geom_tr16_col(l)
+        out.append(geo.geom_tile_offset(row, colh // 8, rb) + 2 * (colh % 8))
+    return out
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_v_transposed_reads_are_conflict_free(geo, d):
+    for nb, h, db, e in itertools.product(range(2), range(2), range(d // 32), range(2)):
+        offs = _v_read_offsets(geo, d, nb, h, db, e)
+        for g0 in range(0, 64, 16):
+            banks = sum((_banks(o, 8) for o in offs[g0:g0 + 16]), [])
+            assert sorted(banks) == list(range(32)), (nb, h, db, e, g0)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_v_transposed_reads_deliver_the_pv_keys(geo, d):
+    """Each 16-lane group addresses a 4-row x 16-column block whose transpose gives lane l the
+    keys pv_key(l, 4e + i) (i = 0..3) of feature column 32*db + l%32."""
+    rb = 2 * d
+    for nb, h, db, e in itertools.product(range(2), range(2), range(d // 32), range(2)):
+        offs = _v_read_offsets(geo, d, nb, h, db, e)
+        for g0 in range(0, 64, 16):
+            # logical (row, col) of what each lane of the group addresses
+            cells = []
+            for l in range(g0, g0 + 16):
+                row = offs[l] // rb
+                phys_chunk = (offs[l] % rb) // 16
+                colh = 8 * geo.geom_swizzle_chunk(row, phys_chunk) + (offs[l] % 16) // 2
+                cells.append((row, colh))
+            rows = sorted({r for r, _ in cells})
+            assert len(rows) == 4 and rows == list(range(rows[0], rows[0] + 4))
+            cols = sorted({c + j for _, c in cells for j in range(4)})
+            assert cols == list(range(cols[0], cols[0] + 16))
+            # the transpose hands lane g0+j column cols[0]+j of rows[0..3]
+            for j in range(16):
+                lane = g0 + j
+                assert cols[0] + j == 32 * db + (lane % 32)
+                for i in range(4):
+                    assert rows[i] == 32 * nb + 16 * h + geo.geom_pv_key(lane, 4 * e + i)
+
+
+def test_p_operand_slots_are_the_score_accumulators(geo):
+    for lane, nb, h, i in itertools.product(range(64), range(4), range(2), range(8)):
+        assert geo.geom_st_key(lane, nb, 8 * h + i) == 32 * nb + 16 * h + geo.geom_pv_key(lane, i)
+
+
+def test_mfma_c_layouts_cover_each_cell_once(geo):
+    cells = {(geo.geom_mfma32_c_row(l, r), geo.geom_mfma32_c_col(l))
+             for l in range(64) for r in range(16)}
+    assert cells == {(m, n) for m in range(32) for n in range(32)}
+    cells = {(geo.geom_mfma16_c_row(l, r), geo.geom_mfma16_c_col(l))
+             for l in range(64) for r in range(4)}
+    assert cells == {(m, n) for m in range(16) for n in range(16)}
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_num_kv_tiles(geo, causal):
+    for n, bq, bk in itertools.product([1, 17, 63, 64, 65, 100, 128, 257, 1000, 2048],
+                                       [64, 128, 256], [32, 64, 128]):
+        for q0 in range(0, n, bq):
+            last_q = min(n, q0 + bq) - 1
+            last_key = last_q if causal else n - 1
+            assert geo.geom_num_kv_tiles(n, q0, bq, bk, causal) == last_key // bk + 1
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_mask_predicates(geo, causal):
+    rows = 32
+    for n, bk in itertools.product([1, 31, 64, 65, 100, 200], [32, 64]):
+        for qw in range(0, n, rows):
+            for kt in range(0, n + bk, bk):
+                masked = [[(key >= n) or (causal and key > q) for key in range(kt, kt + bk)]
+                          for q in range(qw, qw + rows)]
+                anym = any(any(r) for r in masked)
+                allm_causal = all(all(key > q for key in range(kt, kt + bk))
+                                  for q in range(qw, qw + rows))
+                if anym:
+                    assert geo.geom_tile_needs_mask(n, kt, bk, qw, causal)
+                assert geo.geom_tile_fully_masked(kt, qw, rows, causal) == int(
+                    bool(causal) and allm_causal)
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_work_map_is_a_bijection(geo, causal):
+    for bhc, nqb in [(1, 1), (6, 9), (16, 128), (512, 16)]:
+        seen = set()
+        prev = None
+        bh, qb = ctypes.c_int(), ctypes.c_int()
+        for bid in range(bhc * nqb):
+            geo.geom_work_of(bid, bhc, nqb, causal, ctypes.byref(bh), ctypes.byref(qb))
+            assert 0 <= bh.value < bhc and 0 <= qb.value < nqb
+            seen.add((bh.value, qb.value))
+            if causal and prev is not None:
+                assert qb.value <= prev  # longest (highest) query blocks launch first
+            prev = qb.value
+        assert len(seen) == bhc * nqb
