@@ -7,8 +7,8 @@
 // variant name; ValueError (std::invalid_argument) for arguments the launcher rejects, e.g.
 // "head_dim must be 64 or 128". The device check says "CUDA" because torch-ROCm exposes HIP
 // devices under the `cuda` device type.
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/extension.h>
 
 #include <cmath>
@@ -42,7 +42,9 @@ torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torc
                 "q, k, v must be on the same device");
     const uint8_t var = parse_variant(variant);
 
-    const c10::hip::HIPGuard guard(q.device());
+    // torch-ROCm tags HIP devices as DeviceType::CUDA; the masquerading guard and stream
+    // accessors are its HIP implementations for that device type.
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto o = torch::empty_like(q);
 
     const auto head_dim = q.size(3);
@@ -64,7 +66,8 @@ torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torc
     // N = 0 (or any empty dimension) returns an empty output without a launch
     // (csrc/bindings.cpp:60-62).
     if (q.numel() == 0) return o;
-    const int rc = fa_flash_fwd(&p, c10::hip::getCurrentHIPStream().stream());
+    const int rc = fa_flash_fwd(
+        &p, c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream());
     if (rc == FA_EINVAL) throw std::invalid_argument(fa_last_error());
     if (rc != FA_OK) throw std::runtime_error(fa_last_error());
     return o;

@@ -19,6 +19,14 @@ using namespace fa::dev;
 
 namespace {
 
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// Whole-vector bit casts only: a bit cast of a single vector element (an lvalue) miscompiles
+// with this clang (it reads element 0), so results are reinterpreted as a vector first.
+__device__ inline u16x4 bits4(f16x4 v) { return __builtin_bit_cast(u16x4, v); }
+__device__ inline u16x8 bits8(f16x8 v) { return __builtin_bit_cast(u16x8, v); }
+
 // ds_read_b64_tr_b16: LDS holds 256 halves with value i at index i; lane l reads the 8 bytes
 // at half index 4*l. out[4*l + e] = element e returned to lane l.
 __global__ void k_tr16_probe(uint16_t* out) {
@@ -26,8 +34,8 @@ __global__ void k_tr16_probe(uint16_t* out) {
     const int l = threadIdx.x;
     for (int i = l; i < 256; i += 64) lds[i] = static_cast<f16>(i);
     __syncthreads();
-    const f16x4 r = lds_read_tr16(reinterpret_cast<const char*>(lds + 4 * l));
-    for (int e = 0; e < 4; ++e) out[4 * l + e] = __builtin_bit_cast(uint16_t, r[e]);
+    const u16x4 r = bits4(lds_read_tr16(reinterpret_cast<const char*>(lds + 4 * l)));
+    for (int e = 0; e < 4; ++e) out[4 * l + e] = r[e];
 }
 
 // Transposed read as the kernel uses it: a [16 rows][64 cols] fp16 tile (row-major, no
@@ -42,8 +50,8 @@ __global__ void k_tr16_block(const uint16_t* tile, uint16_t* out) {
     const int grp = l >> 4;
     const int row = 4 * grp + fa::geom::tr16_row(l);
     const int colh = 16 * grp + fa::geom::tr16_col(l);
-    const f16x4 r = lds_read_tr16(reinterpret_cast<const char*>(lds + row * 64 + colh));
-    for (int e = 0; e < 4; ++e) out[4 * l + e] = __builtin_bit_cast(uint16_t, r[e]);
+    const u16x4 r = bits4(lds_read_tr16(reinterpret_cast<const char*>(lds + row * 64 + colh)));
+    for (int e = 0; e < 4; ++e) out[4 * l + e] = r[e];
 }
 
 // C(32x32) = A(32x16) B(16x32), fragments loaded in the layout of fa::geom (A, B row-major).
@@ -83,9 +91,9 @@ __global__ void k_exp2(const float* x, float* y, int n) {
 // pack8 (v_cvt_pk_f16_f32): n must be a multiple of 8.
 __global__ void k_pack8(const float* x, uint16_t* y, int n) {
     for (int i = 8 * threadIdx.x; i < n; i += 8 * 64) {
-        const f16x8 p = pack8(x[i], x[i + 1], x[i + 2], x[i + 3], x[i + 4], x[i + 5], x[i + 6],
-                              x[i + 7]);
-        for (int e = 0; e < 8; ++e) y[i + e] = __builtin_bit_cast(uint16_t, p[e]);
+        const u16x8 p = bits8(pack8(x[i], x[i + 1], x[i + 2], x[i + 3], x[i + 4], x[i + 5],
+                                    x[i + 6], x[i + 7]));
+        for (int e = 0; e < 8; ++e) y[i + e] = p[e];
     }
 }
 
