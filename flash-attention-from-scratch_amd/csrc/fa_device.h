@@ -53,6 +53,21 @@ __device__ __forceinline__ void lds_dma16(const void* global_src, char* lds_wave
     __builtin_amdgcn_global_load_lds(global_src, (void FA_LDS*)(lds_wave_base), 16, 0, 0);
 }
 
+// Buffer resource for raw (stride 0) buffer loads of `bytes` bytes from `base`; the hardware
+// range check returns zeros for any access at or past `bytes` (4th descriptor dword of gfx9
+// parts: 0x00020000, 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// 16-byte buffer -> LDS copy (buffer_load_dwordx4 ... lds): lane i reads rsrc + voffset and
+// writes lds_wave_base + 16*i (lds_wave_base wave-uniform). Out-of-range lanes write zeros.
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, int voffset,
+                                              char* lds_wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void FA_LDS*)(lds_wave_base), 16, voffset, 0,
+                                             0, 0);
+}
+
 // Wait until every global load of this wave (including LDS DMA) has landed.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -85,6 +100,17 @@ __device__ __forceinline__ f16x4 pack4(float a0, float a1, float a2, float a3) {
     const f16x2 p0 = __builtin_convertvector(f32x2{a0, a1}, f16x2);
     const f16x2 p1 = __builtin_convertvector(f32x2{a2, a3}, f16x2);
     return f16x4{p0[0], p0[1], p1[0], p1[1]};
+}
+
+// Sum of the eight fp16 values of a packed MFMA operand, accumulated in fp32 onto acc
+// (four v_dot2_f32_f16 against (1, 1)).
+__device__ __forceinline__ float sum8_f16(f16x8 p, float acc) {
+    const f16x2 one = {static_cast<f16>(1.0F), static_cast<f16>(1.0F)};
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 4, 5), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 6, 7), one, acc, false);
+    return acc;
 }
 
 __device__ __forceinline__ bool wave_any(bool pred) {

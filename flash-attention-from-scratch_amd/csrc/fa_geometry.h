@@ -10,26 +10,37 @@
 namespace fa::geom {
 
 // ---- LDS layout of a K or V tile ------------------------------------------------------------
-// A tile is [rows][D] fp16, row-major, 2*D bytes per row (128 B for D=64, 256 B for D=128), so
-// every row starts on the same LDS bank. The 16-byte chunks of a row are permuted by an XOR
-// with a 3-bit function of the row, which breaks the two conflicting access patterns:
-//   * K fragments (ds_read_b128): 8 consecutive lanes read the same logical chunk of 8
-//     consecutive rows; row_xor(row & 7) takes 8 distinct values, so those lanes hit 8
-//     distinct 16-byte bank groups (all 32 banks of a 128-byte LDS cycle).
-//   * V fragments (ds_read_b64_tr_b16): a 16-lane group reads chunks {c, c+1} (c even) of 4
-//     consecutive rows starting at a multiple of 4; row_xor of those rows is {0,2,4,6} + b,
-//     so the 8 chunks read are distinct.
-// Replaces the reference's 8-row XOR swizzle for ldmatrix (csrc/common.cuh:38-42), which is
-// matched to a different access pattern (8-row ldmatrix phases, no transpose reads).
-constexpr int row_xor(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+// A tile is [rows][D] fp16, row-major, row_bytes = 2*D (128 B for D=64, 256 B for D=128). The
+// 16-byte chunks of a row are permuted by an XOR with a function of the row.
+//
+// gfx950 LDS, as measured on MI355X: 64 banks x 4 bytes (256 bytes per cycle); a
+// ds_read_b128 is served 16 lanes at a time and a ds_read_b64_tr_b16 32 lanes at a time, and
+// a group is conflict-free when its lanes hit distinct 4-byte banks (or the same address).
+// The two read patterns of the kernel are:
+//   * K fragments (ds_read_b128): lanes l..l+15 read the same logical chunk of 16 consecutive
+//     rows;
+//   * V^T fragments (ds_read_b64_tr_b16): 32 lanes read logical chunks 4a..4a+3 of 4
+//     consecutive rows starting at a multiple of 4 (8 bytes per lane).
+// D=128 (one row spans all 64 banks): row_xor = 4*(row%4) + (row/4)%4 is a bijection on
+// row%16 (K groups conflict-free) and gives 4 consecutive rows distinct high bits (V groups
+// conflict-free). D=64 (two rows per bank line): row_xor = 4*((row/2)%2) + (row/4)%4 is a
+// bijection on the rows of one parity among 16 (K), and differs in bit 2 between rows r and
+// r+2 (V). Replaces the reference's 8-row XOR for ldmatrix (csrc/common.cuh:38-42), which
+// targets a different bank geometry and access pattern.
+constexpr int row_xor(int row, int row_bytes) {
+    return row_bytes >= 256 ? (((row & 3) << 2) | ((row >> 2) & 3))
+                            : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+}
 
 // Physical chunk slot of logical 16-byte chunk `chunk` of `row`. For a fixed row this is an
 // involution (XOR), so the same function maps physical slots back to logical chunks.
-constexpr int swizzle_chunk(int row, int chunk) { return chunk ^ row_xor(row); }
+constexpr int swizzle_chunk(int row, int chunk, int row_bytes) {
+    return chunk ^ row_xor(row, row_bytes);
+}
 
 // Byte offset of (row, logical chunk) inside a tile with `row_bytes` bytes per row.
 constexpr int tile_offset(int row, int chunk, int row_bytes) {
-    return row * row_bytes + 16 * swizzle_chunk(row, chunk);
+    return row * row_bytes + 16 * swizzle_chunk(row, chunk, row_bytes);
 }
 
 // ---- v_mfma_f32_32x32x16_f16 register layouts (wave64) --------------------------------------
@@ -84,6 +95,24 @@ constexpr bool tile_needs_mask(int n, int kt, int block_k, int qw, bool causal) 
 // Whether every key of the tile is masked for all queries [qw, qw+rows) (causal only).
 constexpr bool tile_fully_masked(int kt, int qw, int rows, bool causal) {
     return causal && kt > qw + rows - 1;
+}
+
+// Number of leading tiles a wave whose queries are [qw, qw+rows) computes: all of them when
+// not causal; when causal, those with a key <= its last query (the rest are fully masked and
+// the wave only takes part in their barriers). 0 for a wave entirely past the sequence.
+constexpr int wave_active_tiles(int n, int qw, int rows, int block_k, int n_tiles, bool causal) {
+    if (qw >= n) return 0;
+    if (!causal) return n_tiles;
+    const int t = (qw + rows - 1) / block_k + 1;
+    return t < n_tiles ? t : n_tiles;
+}
+
+// Length of the leading run of tiles that need no mask for a wave starting at query qw
+// (tile_needs_mask is false exactly for j < this), capped at n_act.
+constexpr int wave_unmasked_tiles(int n, int qw, int block_k, int n_act, bool causal) {
+    int t = n / block_k;
+    if (causal && (qw + 1) / block_k < t) t = (qw + 1) / block_k;
+    return t < n_act ? t : n_act;
 }
 
 // Workgroup id -> (batch*head index, query block). Consecutive ids share the query block and

@@ -32,6 +32,8 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "fa_device.h"
 #include "fa_geometry.h"
@@ -45,12 +47,13 @@ namespace g = fa::geom;
 
 // Compile-time tile shape and options. Counterpart of the reference's Config/Opt pair
 // (csrc/kernels/flash_fwd.cu:70-100), re-derived for 64-wide waves and 32x32 MFMA blocks.
-template <int D_, int BC_, int NW_, bool LAZY_>
+template <int D_, int BC_, int NW_, bool LAZY_, bool PIPE_>
 struct Tile {
     static constexpr int D = D_;            // head dim (64 or 128)
     static constexpr int BC = BC_;          // keys per K/V tile
     static constexpr int NW = NW_;          // wave64s per workgroup
     static constexpr bool LAZY = LAZY_;     // rescale O only when a row max grows by > 2^8
+    static constexpr bool PIPE = PIPE_;     // software-pipelined schedule (QK of j+1 || softmax j)
     static constexpr int BR = 32 * NW;      // query rows per workgroup
     static constexpr int THREADS = 64 * NW;
     static constexpr int ROW_BYTES = 2 * D;
@@ -67,24 +70,229 @@ struct Tile {
     static_assert(LDS_BYTES <= 64 * 1024, "static LDS budget");
 };
 
-// Copies K or V rows [kt, kt + BC) of one head into a swizzled LDS tile. Each wave issues
-// DMA_ITERS 16-byte-per-lane direct loads covering 64 consecutive physical chunk slots; the
-// lane picks the global chunk whose swizzled home is its slot. Rows >= n re-read row n-1
-// (masked later), so no load is ever out of bounds.
+// DMA plan of one wave for a K or V tile: DMA_ITERS 16-byte-per-lane buffer->LDS copies, each
+// filling 64 consecutive physical chunk slots of the swizzled tile; the lane reads the global
+// chunk whose swizzled home is its slot. Offsets are relative to the tile's first row.
 template <class T>
-__device__ __forceinline__ void load_tile(const f16* __restrict__ src, int kt, int n, char* lds,
-                                          int wave, int lane) {
+struct TileDma {
+    int voff[T::DMA_ITERS];  // byte offset of the lane's source chunk
+    int lds0[T::DMA_ITERS];  // wave-uniform LDS byte offset of the wave's 64 slots
+    __device__ __forceinline__ TileDma(int wave, int lane) {
 #pragma unroll
-    for (int it = 0; it < T::DMA_ITERS; ++it) {
-        const int slot0 = (it * T::NW + wave) * 64;  // wave-uniform
-        const int slot = slot0 + lane;
-        const int row = slot / T::CPR;
-        const int chunk = g::swizzle_chunk(row, slot % T::CPR);
-        const int grow = min(kt + row, n - 1);
-        lds_dma16(src + static_cast<size_t>(grow) * T::D + chunk * 8, lds + slot0 * 16);
+        for (int it = 0; it < T::DMA_ITERS; ++it) {
+            const int slot0 = (it * T::NW + wave) * 64;
+            const int slot = slot0 + lane;
+            const int row = slot / T::CPR;
+            voff[it] = row * T::ROW_BYTES +
+                       16 * g::swizzle_chunk(row, slot % T::CPR, T::ROW_BYTES);
+            lds0[it] = slot0 * 16;
+        }
+    }
+};
+
+// Copies K or V rows [kt, kt + BC) of one head into a swizzled LDS tile. The buffer resource
+// covers rows [kt, n) only, so rows >= n are zero-filled by the hardware range check (their
+// scores are masked, and zero V rows keep 0 * garbage from ever forming a NaN); the per-tile
+// offset lives in the scalar resource, so a refill costs no VALU work.
+template <class T>
+__device__ __forceinline__ void load_tile(const f16* head, int kt, int n, char* lds,
+                                          const TileDma<T>& dma) {
+    const char* base = reinterpret_cast<const char*>(head) + static_cast<size_t>(kt) * T::ROW_BYTES;
+    const auto rsrc = make_rsrc(base, max(0, n - kt) * T::ROW_BYTES);
+#pragma unroll
+    for (int it = 0; it < T::DMA_ITERS; ++it) lds_dma16_buf(rsrc, dma.voff[it], lds + dma.lds0[it]);
+}
+
+// ---- per-wave building blocks -----------------------------------------------------------------
+// Lane-dependent LDS offsets of the MFMA operands. The row XOR depends on row % 16 only and
+// every row offset added later (32-key blocks, 16-key steps) is a multiple of 16 rows, so those
+// become immediate offsets of the ds_read instructions.
+template <class T>
+struct Frag {
+    int koff[T::KK];     // K fragment kk: row lane%32, logical chunk 2*kk + lane/32
+    int voff[T::DB][2];  // V^T fragment (db, e): rows 8e + 4*(lane/32) + tr16_row, 16 columns
+    __device__ __forceinline__ explicit Frag(int lane) {
+        const int col = lane & 31;
+        const int hi = lane >> 5;
+#pragma unroll
+        for (int kk = 0; kk < T::KK; ++kk) koff[kk] = g::tile_offset(col, 2 * kk + hi, T::ROW_BYTES);
+#pragma unroll
+        for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int row = 8 * e + 4 * hi + g::tr16_row(lane);
+                const int c = 32 * db + 16 * ((lane >> 4) & 1) + g::tr16_col(lane);  // halves
+                voff[db][e] = g::tile_offset(row, c >> 3, T::ROW_BYTES) + 2 * (c & 7);
+            }
+    }
+};
+
+// Q^T operand: lane holds Q[qrow][16*kk + 8*(lane/32) .. +7] for every kk (32 VGPRs at D=128).
+template <class T>
+__device__ __forceinline__ void load_q(const f16* qh, int qrow, int n, int lane, int negate_q,
+                                       f16x8 (&qf)[T::KK]) {
+    const f16* src = qh + static_cast<size_t>(min(qrow, n - 1)) * T::D + 8 * (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < T::KK; ++kk) qf[kk] = *reinterpret_cast<const f16x8*>(src + 16 * kk);
+    if (negate_q) {
+#pragma unroll
+        for (int kk = 0; kk < T::KK; ++kk) qf[kk] = -qf[kk];
     }
 }
 
+// S^T = K Q^T for one tile: NB x KK MFMAs, K fragments from LDS.
+template <class T>
+__device__ __forceinline__ void qk_tile(const char* kl, const Frag<T>& fr,
+                                        const f16x8 (&qf)[T::KK], f32x16 (&s)[T::NB]) {
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) {
+        s[nb] = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < T::KK; ++kk) {
+            const f16x8 a =
+                *reinterpret_cast<const f16x8*>(kl + fr.koff[kk] + nb * 32 * T::ROW_BYTES);
+            s[nb] = mfma32(a, qf[kk], s[nb]);
+        }
+    }
+}
+
+// Keys >= n, and (causal) keys right of the lane's query, get -inf.
+template <class T, bool CAUSAL>
+__device__ __forceinline__ void mask_tile(f32x16 (&s)[T::NB], int kt, int n, int qrow, int lane) {
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kt + g::st_key(lane, nb, r);
+            const bool masked = key >= n || (CAUSAL && key > qrow);
+            s[nb][r] = masked ? -INFINITY : s[nb][r];
+        }
+}
+
+// Online softmax of one tile in base 2 (csrc/kernels/flash_fwd.cu:347-422 is the reference's).
+// Updates the running max m and the lane's partial row sum l, and returns in `rescale`
+// (wave-uniform) whether O must be multiplied by `alpha` before this tile's P.V is added.
+// Without LAZY, O is rescaled whenever a row max grows; with LAZY only when one grows by more
+// than 8 (log2 units), otherwise the stale max stays in use and p may reach 2^8 (exact: l and
+// O see the same p). Selects instead of branches keep this straight-line code.
+template <class T>
+__device__ __forceinline__ void softmax_tile(const f32x16 (&s)[T::NB], float scale_log2,
+                                             float& m_run, float& l_run, float& alpha,
+                                             bool& rescale, f16x8 (&p)[T::NB][2]) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[nb][r]);
+    mx = max_xor32(mx) * scale_log2;  // both halves of the wave agree on the query's tile max
+    rescale = wave_any(T::LAZY ? (mx > m_run + 8.0F) : (mx > m_run));
+    const float m_new = rescale ? fmaxf(m_run, mx) : m_run;
+    // m_new is -inf only for a row that has seen nothing but masked keys; use 0 there so that
+    // -inf - -inf never forms a NaN (its p values are exp2(-inf) = 0).
+    const float m_use = (m_new == -INFINITY) ? 0.0F : m_new;
+    alpha = exp2_fast(m_run - m_use);
+    m_run = m_new;
+    // The row sum is taken over the fp16 P values the P.V MFMA consumes (v_dot2 with fp32
+    // accumulation), so numerator and denominator of O see identical weights.
+    float sum = 0.0F;
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) {
+        float e[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[r] = exp2_fast(fmaf(s[nb][r], scale_log2, -m_use));
+        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
+        sum = sum8_f16(p[nb][1], sum8_f16(p[nb][0], sum));
+    }
+    l_run = (rescale ? l_run * alpha : l_run) + sum;
+}
+
+template <class T>
+__device__ __forceinline__ void rescale_o(f32x16 (&oacc)[T::DB], float alpha) {
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db) oacc[db] *= alpha;
+}
+
+// O^T += V^T P^T for one tile: NB x 2 x DB MFMAs, V^T fragments by transposed LDS reads.
+template <class T>
+__device__ __forceinline__ void pv_tile(const char* vl, const Frag<T>& fr,
+                                        const f16x8 (&p)[T::NB][2], f32x16 (&oacc)[T::DB]) {
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int db = 0; db < T::DB; ++db) {
+                const char* base = vl + (32 * nb + 16 * h) * T::ROW_BYTES;
+                const f16x4 lo = lds_read_tr16(base + fr.voff[db][0]);
+                const f16x4 up = lds_read_tr16(base + fr.voff[db][1]);
+                const f16x8 a = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+                oacc[db] = mfma32(a, p[nb][h], oacc[db]);
+            }
+}
+
+// K fragments of a whole tile into registers (NB*KK operands of 4 VGPRs).
+template <class T>
+__device__ __forceinline__ void load_k_frags(const char* kl, const Frag<T>& fr,
+                                             f16x8 (&kf)[T::NB][T::KK]) {
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int kk = 0; kk < T::KK; ++kk)
+            kf[nb][kk] =
+                *reinterpret_cast<const f16x8*>(kl + fr.koff[kk] + nb * 32 * T::ROW_BYTES);
+}
+
+// V^T fragments of a whole tile into registers (NB*2*DB operands of 4 VGPRs), so their LDS
+// latency can be covered by other work before pv_frags consumes them.
+template <class T>
+__device__ __forceinline__ void load_v_frags(const char* vl, const Frag<T>& fr,
+                                             f16x8 (&vf)[T::NB][2][T::DB]) {
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int db = 0; db < T::DB; ++db) {
+                const char* base = vl + (32 * nb + 16 * h) * T::ROW_BYTES;
+                const f16x4 lo = lds_read_tr16(base + fr.voff[db][0]);
+                const f16x4 up = lds_read_tr16(base + fr.voff[db][1]);
+                vf[nb][h][db] = f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+            }
+}
+
+template <class T>
+__device__ __forceinline__ void pv_frags(const f16x8 (&vf)[T::NB][2][T::DB],
+                                         const f16x8 (&p)[T::NB][2], f32x16 (&oacc)[T::DB]) {
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int db = 0; db < T::DB; ++db) oacc[db] = mfma32(vf[nb][h][db], p[nb][h], oacc[db]);
+}
+
+// O = acc / l as fp16 (RNE) for the lane's query row, if it is < n. The lane holds feature
+// columns 32*db + 8*rq + 4*(lane/32) + 0..3: one 8-byte store each.
+template <class T>
+__device__ __forceinline__ void store_o(f16* oh, int qrow, int n, int lane, float l_run,
+                                        const f32x16 (&oacc)[T::DB]) {
+    const float l_tot = sum_xor32(l_run);
+    const float inv = (l_tot > 0.0F) ? (1.0F / l_tot) : 0.0F;
+    if (qrow >= n) return;
+    f16* dst = oh + static_cast<size_t>(qrow) * T::D + 4 * (lane >> 5);
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+            const f32x16& a = oacc[db];
+            *reinterpret_cast<f16x4*>(dst + 32 * db + 8 * rq) = pack4(
+                a[4 * rq] * inv, a[4 * rq + 1] * inv, a[4 * rq + 2] * inv, a[4 * rq + 3] * inv);
+        }
+}
+
+// ---- kernel, simple schedule (the "baseline" build) -----------------------------------------
+// Per tile: barrier, prefetch tile j+1, then S = QK^T, softmax, O += PV in sequence.
 template <class T, bool CAUSAL>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
@@ -93,56 +301,25 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
-    const int col = lane & 31;  // this lane's query within the wave's 32
-    const int hi = lane >> 5;   // which half of the wave
-
     const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
-    const f16* qh = q + head;
     const f16* kh = k + head;
     const f16* vh = v + head;
-    f16* oh = o + head;
-
     const int q0 = w.qb * T::BR;
-    const int qw = q0 + wave * 32;  // first query of this wave
-    const int qrow = qw + col;      // this lane's query
+    const int qw = q0 + wave * 32;       // first query of this wave
+    const int qrow = qw + (lane & 31);   // this lane's query
     const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
 
     // LDS: [K0 | K1 | V0 | V1]; buffer b of K at b*TILE_BYTES, of V at (2+b)*TILE_BYTES.
     auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
     auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
 
-    // Prefetch tile 0 while Q is fetched into registers.
-    load_tile<T>(kh, 0, n, kbuf(0), wave, lane);
-    load_tile<T>(vh, 0, n, vbuf(0), wave, lane);
-
-    // Q^T operand: lane holds Q[qrow][16*kk + 8*hi .. +7] for every kk (32 VGPRs at D=128).
+    const TileDma<T> dma(wave, lane);
+    load_tile<T>(kh, 0, n, kbuf(0), dma);
+    load_tile<T>(vh, 0, n, vbuf(0), dma);
     f16x8 qf[T::KK];
-    {
-        const f16* src = qh + static_cast<size_t>(min(qrow, n - 1)) * T::D + 8 * hi;
-#pragma unroll
-        for (int kk = 0; kk < T::KK; ++kk) {
-            qf[kk] = *reinterpret_cast<const f16x8*>(src + 16 * kk);
-            if (negate_q) qf[kk] = -qf[kk];
-        }
-    }
-
-    // Per-lane LDS byte offsets. K fragment (nb, kk): row 32*nb + col, logical chunk 2*kk + hi.
-    // Only the low 3 chunk bits are swizzled, so chunk 2*kk+hi splits into an immediate part
-    // 8*(kk/4) and a lane part ((2*(kk%4)+hi) ^ row_xor(col)).
-    int koff[4];
-#pragma unroll
-    for (int kq = 0; kq < 4; ++kq)
-        koff[kq] = col * T::ROW_BYTES + 16 * ((2 * kq + hi) ^ g::row_xor(col));
-    // V^T fragment (nb, h, db, half-read e): rows 32*nb + 16*h + 8*e + 4*hi + tr16_row(lane),
-    // columns 32*db + 16*((lane>>4)&1) + tr16_col(lane). row & 7 = 4*hi + tr16_row(lane).
-    const int vrow = 4 * hi + g::tr16_row(lane);
-    int voff[2];
-#pragma unroll
-    for (int dpar = 0; dpar < 2; ++dpar) {
-        const int c = 32 * dpar + 16 * ((lane >> 4) & 1) + g::tr16_col(lane);  // column in halves
-        voff[dpar] = vrow * T::ROW_BYTES + 16 * ((c >> 3) ^ g::row_xor(vrow)) + 2 * (c & 7);
-    }
+    load_q<T>(q + head, qrow, n, lane, negate_q, qf);
+    const Frag<T> fr(lane);
 
     f32x16 oacc[T::DB];
 #pragma unroll
@@ -154,113 +331,282 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         wait_vmem();
         __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
         if (j + 1 < n_tiles) {
-            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf((j + 1) & 1), wave, lane);
-            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), wave, lane);
+            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf((j + 1) & 1), dma);
+            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), dma);
         }
         const int kt = j * T::BC;
         if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) continue;  // wave-uniform
-        const char* kl = kbuf(j & 1);
-        const char* vl = vbuf(j & 1);
-
-        // ---- S^T = K Q^T ------------------------------------------------------------------
         f32x16 s[T::NB];
-#pragma unroll
-        for (int nb = 0; nb < T::NB; ++nb) {
-            s[nb] = f32x16{};
-#pragma unroll
-            for (int kk = 0; kk < T::KK; ++kk) {
-                const f16x8 a = *reinterpret_cast<const f16x8*>(
-                    kl + koff[kk & 3] + nb * 32 * T::ROW_BYTES + 128 * (kk >> 2));
-                s[nb] = mfma32(a, qf[kk], s[nb]);
-            }
-        }
-
-        // ---- mask (tail tile, causal diagonal) ---------------------------------------------
-        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) {
-#pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kt + g::st_key(lane, nb, r);
-                    const bool masked = key >= n || (CAUSAL && key > qrow);
-                    s[nb][r] = masked ? -INFINITY : s[nb][r];
-                }
-        }
-
-        // ---- online softmax (base 2) -------------------------------------------------------
-        float mx = -INFINITY;
-#pragma unroll
-        for (int nb = 0; nb < T::NB; ++nb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[nb][r]);
-        mx = max_xor32(mx) * scale_log2;  // both halves now agree on the query's tile max
-
-        const bool grow = T::LAZY ? (mx > m_run + 8.0F) : (mx > m_run);
-        if (wave_any(grow)) {
-            const float m_new = fmaxf(m_run, mx);
-            // m_new is -inf only for a row that has seen nothing but masked keys; use 0 there so
-            // that -inf - -inf never forms a NaN (its p values are exp2(-inf) = 0).
-            const float alpha = exp2_fast(m_run - (m_new == -INFINITY ? 0.0F : m_new));
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < T::DB; ++db) oacc[db] *= alpha;
-        }
-        const float m_use = (m_run == -INFINITY) ? 0.0F : m_run;
-
+        qk_tile<T>(kbuf(j & 1), fr, qf, s);
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
+        float alpha;
+        bool rescale;
+        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale_o<T>(oacc, alpha);
+        pv_tile<T>(vbuf(j & 1), fr, p, oacc);
+    }
+    store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+}
+
+// Scheduler pattern: N times {one MFMA, then up to VALU_PER VALU instructions}. Masks of
+// __builtin_amdgcn_sched_group_barrier (LLVM AMDGPU): 0x008 MFMA, 0x002 VALU.
+#ifndef FA_VALU_PER_MFMA
+#define FA_VALU_PER_MFMA 10
+#endif
+template <int VALU_PER, int... I>
+__device__ __forceinline__ void sched_mfma_valu(std::integer_sequence<int, I...>) {
+    ((__builtin_amdgcn_sched_group_barrier(0x008, 1, 0),
+      __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER + 0 * I, 0)),
+     ...);
+}
+
+// Region pattern of the steady-state iteration: the K fragment reads, two {MFMA, VALU}
+// stages, then the V^T fragment reads and the DMA refill (0x100 DS read, 0x020 VMEM read),
+// then the remaining stages. The K reads come first so the first MFMA waits for them only.
+template <int VALU_PER, int NK, int NV, int NDMA, int M>
+__device__ __forceinline__ void sched_steady_region() {
+    __builtin_amdgcn_sched_group_barrier(0x100, NK, 0);
+    sched_mfma_valu<VALU_PER>(std::make_integer_sequence<int, 2>{});
+    __builtin_amdgcn_sched_group_barrier(0x100, NV, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, NDMA, 0);
+    sched_mfma_valu<VALU_PER>(std::make_integer_sequence<int, M - 2>{});
+}
+
+// ---- QK of tile j+1 interleaved with the softmax of tile j -------------------------------------
+// NB*KK stages; stage m issues MFMA m of S^T_{j+1} = K_{j+1} Q^T and then one slice of tile j's
+// softmax: the first quarter of the stages reduce the row max over the lane's 16*NB scores, the
+// next one combines the halves of the wave and fixes the new max, and the rest compute the
+// exponentials; the fp16 packing and row sums follow the last stage. The caller's sched_group_barrier pattern makes the
+// scheduler emit each MFMA followed by about FA_VALU_PER_MFMA VALU instructions, so the VALU
+// work issues while the MFMAs run. Same arithmetic as mask-free softmax_tile.
+template <class T>
+__device__ __forceinline__ void qk_softmax_interleaved(
+    const f16x8 (&kf)[T::NB][T::KK], const f16x8 (&qf)[T::KK], const f32x16 (&s)[T::NB],
+    float scale_log2, float& m_run, float& l_run, float& alpha, bool& rescale,
+    f32x16 (&s_next)[T::NB], f16x8 (&p)[T::NB][2]) {
+    constexpr int M = T::NB * T::KK;   // MFMA stages
+    constexpr int E = 16 * T::NB;      // scores per lane
+    constexpr int M1 = M / 4 > 0 ? M / 4 : 1;
+    constexpr int PER_MAX = (E + M1 - 1) / M1;
+    constexpr int M2 = M - M1 - 1;
+    constexpr int PER_EXP = (E + M2 - 1) / M2;
+    static_assert(M2 >= 1, "need at least one exponential stage");
+    float mx = -INFINITY;
+    float m_use = 0.0F;
+    float sum = 0.0F;
+    float pe[E];
 #pragma unroll
-        for (int nb = 0; nb < T::NB; ++nb) {
-            float e[16];
+    for (int nb = 0; nb < T::NB; ++nb) s_next[nb] = f32x16{};
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                e[r] = exp2_fast(fmaf(s[nb][r], scale_log2, -m_use));
-                l_run += e[r];
-            }
-            p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
-            p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
+    for (int m = 0; m < M; ++m) {
+        s_next[m / T::KK] = mfma32(kf[m / T::KK][m % T::KK], qf[m % T::KK], s_next[m / T::KK]);
+        if (m < M1) {
+#pragma unroll
+            for (int e = m * PER_MAX; e < (m + 1) * PER_MAX && e < E; ++e)
+                mx = fmaxf(mx, s[e / 16][e % 16]);
+        } else if (m == M1) {
+            mx = max_xor32(mx) * scale_log2;
+            rescale = wave_any(T::LAZY ? (mx > m_run + 8.0F) : (mx > m_run));
+            const float m_new = rescale ? fmaxf(m_run, mx) : m_run;
+            m_use = (m_new == -INFINITY) ? 0.0F : m_new;
+            alpha = exp2_fast(m_run - m_use);
+            m_run = m_new;
+        } else {
+            const int st = m - M1 - 1;
+#pragma unroll
+            for (int e = st * PER_EXP; e < (st + 1) * PER_EXP && e < E; ++e)
+                pe[e] = exp2_fast(fmaf(s[e / 16][e % 16], scale_log2, -m_use));
         }
+    }
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) {
+        const float* e = pe + 16 * nb;
+        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
+        sum = sum8_f16(p[nb][1], sum8_f16(p[nb][0], sum));
+    }
+    l_run = (rescale ? l_run * alpha : l_run) + sum;
+    // Empty asm that reads P and l: keeps their computation in this block. Without it LLVM
+    // sinks the exponentials past the caller's (rarely taken) rescale branch, behind the MFMAs.
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) asm volatile("" ::"v"(p[nb][0]), "v"(p[nb][1]));
+    asm volatile("" ::"v"(l_run));
+}
 
-        // ---- O^T += V^T P^T ----------------------------------------------------------------
+// ---- kernel, software-pipelined schedule (the "opt" build) ----------------------------------
+// Each wave overlaps the S^T = K Q^T MFMAs of tile j+1 with the softmax VALU work of tile j in
+// one straight-line block, then issues tile j's P.V MFMAs; with two waves per SIMD the matrix
+// pipe is fed while either wave is in its softmax. K and V are double-buffered separately:
+// at the barrier of iteration j, K_{j+2} and V_{j+1} are requested (their buffers were last
+// read by QK_j and PV_{j-1}, both finished before that barrier), and both land before the
+// next barrier. Tiles run in two loops: a steady-state loop over tiles that need no mask and
+// whose successor is visible to the wave, and a general loop for the rest (diagonal and tail
+// tiles, and tiles a causal wave only waits through).
+template <class T, bool CAUSAL>
+__global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ o, int n, int bh_count, int n_qblocks, float scale_log2, int negate_q) {
+    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_uniform(threadIdx.x >> 6);
+    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
+    const f16* kh = k + head;
+    const f16* vh = v + head;
+    const int q0 = w.qb * T::BR;
+    const int qw = q0 + wave * 32;
+    const int qrow = qw + (lane & 31);
+    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    // Tiles this wave computes (the rest it only waits through), and the leading run of them
+    // that needs no masking.
+    const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
+    const int n_plain = g::wave_unmasked_tiles(n, qw, T::BC, n_act, CAUSAL);
+
+    auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
+    auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
+
+    const TileDma<T> dma(wave, lane);
+    load_tile<T>(kh, 0, n, kbuf(0), dma);
+    load_tile<T>(vh, 0, n, vbuf(0), dma);
+    if (n_tiles > 1) load_tile<T>(kh, T::BC, n, kbuf(1), dma);
+    f16x8 qf[T::KK];
+    load_q<T>(q + head, qrow, n, lane, negate_q, qf);
+    const Frag<T> fr(lane);
+
+    f32x16 oacc[T::DB];
 #pragma unroll
-        for (int nb = 0; nb < T::NB; ++nb)
+    for (int db = 0; db < T::DB; ++db) oacc[db] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0F;
+
+    wait_vmem();
+    __syncthreads();
+    f32x16 s[T::NB];
+    f32x16 s2[T::NB];
+    if (n_act > 0) qk_tile<T>(kbuf(0), fr, qf, s);
+
+    // Steady state: tile j unmasked, tile j+1 active. The LDS reads of the iteration (K
+    // fragments of tile j+1, V^T fragments of tile j) precede the DMA refill in program order:
+    // the compiler cannot tell that the refill writes the other buffers and would otherwise
+    // make the transposed reads wait for it. The refill (K_{j+2} into K buffer j%2, V_{j+1}
+    // into V buffer (j+1)%2; both buffers were last read before this iteration's barrier) is
+    // unconditional so it shares the scheduling region; a K tile past the end reads as zeros
+    // into a buffer nobody reads again. The QK MFMAs of tile j+1 are interleaved with tile j's
+    // softmax (sched_steady_region); then, after the rarely taken rescale branch, tile j's PV
+    // MFMAs. Two tiles per trip, so every buffer address is an immediate and the score
+    // registers alternate between s and s2 without copies.
+    auto steady = [&](int jj, auto parity, f32x16(&s_cur)[T::NB], f32x16(&s_nxt)[T::NB]) {
+        constexpr int PAR = decltype(parity)::value;  // jj % 2
+        wait_vmem();
+        __syncthreads();
+        f16x8 kf[T::NB][T::KK];
+        load_k_frags<T>(kbuf(1 - PAR), fr, kf);
+        f16x8 vf[T::NB][2][T::DB];
+        load_v_frags<T>(vbuf(PAR), fr, vf);
+        load_tile<T>(kh, (jj + 2) * T::BC, n, kbuf(PAR), dma);
+        load_tile<T>(vh, (jj + 1) * T::BC, n, vbuf(1 - PAR), dma);
+        f16x8 p[T::NB][2];
+        float alpha;
+        bool rescale;
+        qk_softmax_interleaved<T>(kf, qf, s_cur, scale_log2, m_run, l_run, alpha, rescale, s_nxt,
+                                  p);
+        sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
+                            2 * T::DMA_ITERS, T::NB * T::KK>();
+        if (rescale) rescale_o<T>(oacc, alpha);
+        pv_frags<T>(vf, p, oacc);
+    };
+    const int n_steady = min(n_plain, n_act - 1);
+    int j = 0;
+    for (; j + 2 <= n_steady; j += 2) {
+        steady(j, std::integral_constant<int, 0>{}, s, s2);
+        steady(j + 1, std::integral_constant<int, 1>{}, s2, s);
+    }
+    if (j < n_steady) {
+        steady(j, std::integral_constant<int, 0>{}, s, s2);
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int db = 0; db < T::DB; ++db) {
-                    const char* base =
-                        vl + voff[db & 1] + (32 * nb + 16 * h) * T::ROW_BYTES + 128 * (db >> 1);
-                    const f16x4 lo = lds_read_tr16(base);
-                    const f16x4 up = lds_read_tr16(base + 8 * T::ROW_BYTES);
-                    const f16x8 a = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-                    oacc[db] = mfma32(a, p[nb][h], oacc[db]);
-                }
+        for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+        ++j;
     }
 
-    // ---- epilogue: O = acc / l, fp16 (RNE), rows < n ----------------------------------------
-    const float l_tot = sum_xor32(l_run);
-    const float inv = (l_tot > 0.0F) ? (1.0F / l_tot) : 0.0F;
-    if (qrow < n) {
-        f16* dst = oh + static_cast<size_t>(qrow) * T::D + 4 * hi;
+    // General tiles (diagonal, tail, or only waited through); same read-then-refill order.
+    for (; j < n_tiles; ++j) {
+        wait_vmem();
+        __syncthreads();
+        const bool act = j < n_act;
+        const bool act_next = j + 1 < n_act;
+        f16x8 kf[T::NB][T::KK];
+        f16x8 vf[T::NB][2][T::DB];
+        if (act_next) load_k_frags<T>(kbuf((j + 1) & 1), fr, kf);
+        if (act) load_v_frags<T>(vbuf(j & 1), fr, vf);
+        if (j + 2 < n_tiles) load_tile<T>(kh, (j + 2) * T::BC, n, kbuf(j & 1), dma);
+        if (j + 1 < n_tiles) load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), dma);
+        if (!act) continue;  // wave-uniform: fully masked for this wave (causal)
+        if (act_next) {
 #pragma unroll
-        for (int db = 0; db < T::DB; ++db)
+            for (int nb = 0; nb < T::NB; ++nb) {
+                s2[nb] = f32x16{};
 #pragma unroll
-            for (int rq = 0; rq < 4; ++rq) {
-                const f32x16& a = oacc[db];
-                *reinterpret_cast<f16x4*>(dst + 32 * db + 8 * rq) =
-                    pack4(a[4 * rq] * inv, a[4 * rq + 1] * inv, a[4 * rq + 2] * inv,
-                          a[4 * rq + 3] * inv);
+                for (int kk = 0; kk < T::KK; ++kk) s2[nb] = mfma32(kf[nb][kk], qf[kk], s2[nb]);
             }
+        }
+        const int kt = j * T::BC;
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
+        f16x8 p[T::NB][2];
+        float alpha;
+        bool rescale;
+        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale_o<T>(oacc, alpha);
+        pv_frags<T>(vf, p, oacc);
+        if (act_next) {
+#pragma unroll
+            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+        }
     }
+    store_o<T>(o + head, qrow, n, lane, l_run, oacc);
 }
 
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
-// (csrc/kernels/flash_fwd.cu:597-612), chosen for MI355X.
-using BaseD64 = Tile<64, 64, 4, false>;
-using BaseD128 = Tile<128, 64, 4, false>;
-using OptD64 = Tile<64, 64, 4, true>;
-using OptD128 = Tile<128, 64, 4, true>;
+// (csrc/kernels/flash_fwd.cu:597-612), chosen for MI355X by a sweep. Each entry is
+// "BC, NW, LAZY, PIPE" and can be overridden at build time with -DFA_<NAME>="bc, nw, lazy, pipe"
+// (the counterpart of bench/tune.sh, which rewrites those lines with sed).
+#ifndef FA_BASE_D64
+#define FA_BASE_D64 64, 4, false, false
+#endif
+#ifndef FA_BASE_D128
+#define FA_BASE_D128 64, 4, false, false
+#endif
+#ifndef FA_OPT_D64
+#define FA_OPT_D64 64, 4, true, true
+#endif
+#ifndef FA_OPT_D64_CAUSAL
+#define FA_OPT_D64_CAUSAL 64, 4, true, true
+#endif
+#ifndef FA_OPT_D128
+#define FA_OPT_D128 32, 8, true, true
+#endif
+#ifndef FA_OPT_D128_CAUSAL
+#define FA_OPT_D128_CAUSAL 32, 8, true, true
+#endif
+using BaseD64 = Tile<64, FA_BASE_D64>;
+using BaseD128 = Tile<128, FA_BASE_D128>;
+using OptD64 = Tile<64, FA_OPT_D64>;
+using OptD64Causal = Tile<64, FA_OPT_D64_CAUSAL>;
+using OptD128 = Tile<128, FA_OPT_D128>;
+using OptD128Causal = Tile<128, FA_OPT_D128_CAUSAL>;
+
+// One tile per (head dim, causal) for a variant (the reference's KernelSet,
+// csrc/kernels/flash_fwd.cu:582-591).
+template <class D64, class D64C, class D128, class D128C>
+struct KernelSet {
+    template <bool CAUSAL, int D>
+    using Pick = std::conditional_t<
+        D == 64, std::conditional_t<CAUSAL, D64C, D64>, std::conditional_t<CAUSAL, D128C, D128>>;
+};
+using BaseSet = KernelSet<BaseD64, BaseD64, BaseD128, BaseD128>;
+using OptSet = KernelSet<OptD64, OptD64Causal, OptD128, OptD128Causal>;
 
 template <class T>
 constexpr fa_tile_info info_of() {
@@ -286,34 +632,48 @@ int launch(const fa_params& p, hipStream_t stream, float scale_log2, int negate_
     int nqb = n_qblocks;
     void* args[] = {&qp, &kp, &vp, &op, &n, &bh, &nqb, &scale_log2, &negate_q};
     const dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh));
-    const hipError_t err =
-        hipLaunchKernel(reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL>), grid,
-                        dim3(T::THREADS), args, 0, stream);
+    const void* fn;
+    if constexpr (T::PIPE) {
+        fn = reinterpret_cast<const void*>(&flash_fwd_pipelined<T, CAUSAL>);
+    } else {
+        fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL>);
+    }
+    const hipError_t err = hipLaunchKernel(fn, grid, dim3(T::THREADS), args, 0, stream);
     if (err != hipSuccess) {
         return fail(FA_EHIP, std::string("flash_fwd: HIP launch failed: ") + hipGetErrorString(err));
     }
     return FA_OK;
 }
 
-template <class T64, class T128>
+template <class Set, int D>
+int dispatch_d(const fa_params& p, hipStream_t s, float scale_log2, int negate_q) {
+    return p.causal
+               ? launch<typename Set::template Pick<true, D>, true>(p, s, scale_log2, negate_q)
+               : launch<typename Set::template Pick<false, D>, false>(p, s, scale_log2, negate_q);
+}
+
+template <class Set>
 int dispatch(const fa_params& p, hipStream_t s, float scale_log2, int negate_q) {
-    if (p.head_dim == 64) {
-        return p.causal ? launch<T64, true>(p, s, scale_log2, negate_q)
-                        : launch<T64, false>(p, s, scale_log2, negate_q);
-    }
-    return p.causal ? launch<T128, true>(p, s, scale_log2, negate_q)
-                    : launch<T128, false>(p, s, scale_log2, negate_q);
+    return p.head_dim == 64 ? dispatch_d<Set, 64>(p, s, scale_log2, negate_q)
+                            : dispatch_d<Set, 128>(p, s, scale_log2, negate_q);
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
 
-bool tile_of(int head_dim, int variant, fa_tile_info* out) {
-    if (head_dim != 64 && head_dim != 128) return false;
-    if (variant == FA_VARIANT_BASELINE) {
-        *out = head_dim == 64 ? info_of<BaseD64>() : info_of<BaseD128>();
-    } else {
-        *out = head_dim == 64 ? info_of<OptD64>() : info_of<OptD128>();
+template <class Set>
+fa_tile_info info_for(int head_dim, bool causal) {
+    if (head_dim == 64) {
+        return causal ? info_of<typename Set::template Pick<true, 64>>()
+                      : info_of<typename Set::template Pick<false, 64>>();
     }
+    return causal ? info_of<typename Set::template Pick<true, 128>>()
+                  : info_of<typename Set::template Pick<false, 128>>();
+}
+
+bool tile_of(int head_dim, bool causal, int variant, fa_tile_info* out) {
+    if (head_dim != 64 && head_dim != 128) return false;
+    *out = variant == FA_VARIANT_BASELINE ? info_for<BaseSet>(head_dim, causal)
+                                          : info_for<OptSet>(head_dim, causal);
     return true;
 }
 
@@ -328,12 +688,11 @@ const char* fa_version(void) { return "fa_hip 0.1.0 gfx950"; }
 
 int fa_tile_config(int32_t head_dim, int32_t causal, int32_t variant, fa_tile_info* out) {
     fa::g_last_error.clear();
-    (void)causal;
     if (out == nullptr) return fa::fail(FA_EINVAL, "fa_tile_config: out must not be NULL");
     if (variant < FA_VARIANT_BASELINE || variant > FA_VARIANT_FP16ACC) {
         return fa::fail(FA_EINVAL, "fa_tile_config: unknown variant");
     }
-    if (!fa::tile_of(head_dim, variant, out)) {
+    if (!fa::tile_of(head_dim, causal != 0, variant, out)) {
         return fa::fail(FA_EINVAL, "fa_tile_config: head_dim must be 64 or 128, got " +
                                        std::to_string(head_dim));
     }
@@ -374,7 +733,7 @@ int fa_flash_fwd(const fa_params* params, void* stream) {
         return fail(FA_EINVAL, "flash_fwd: seqlen * head_dim must be below 2^31");
     }
     fa_tile_info t{};
-    fa::tile_of(p.head_dim, p.variant, &t);
+    fa::tile_of(p.head_dim, p.causal != 0, p.variant, &t);
     const int64_t blocks = static_cast<int64_t>(p.batch) * p.heads *
                            ((static_cast<int64_t>(p.seqlen) + t.block_q - 1) / t.block_q);
     if (blocks > INT32_MAX) {
@@ -396,9 +755,9 @@ int fa_flash_fwd(const fa_params* params, void* stream) {
 
     auto s = static_cast<hipStream_t>(stream);
     if (p.variant == FA_VARIANT_BASELINE) {
-        return fa::dispatch<fa::BaseD64, fa::BaseD128>(p, s, scale_log2, negate_q);
+        return fa::dispatch<fa::BaseSet>(p, s, scale_log2, negate_q);
     }
-    return fa::dispatch<fa::OptD64, fa::OptD128>(p, s, scale_log2, negate_q);
+    return fa::dispatch<fa::OptSet>(p, s, scale_log2, negate_q);
 }
 
 }  // extern "C"

@@ -41,6 +41,9 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Keep MFMA accumulators in ordinary VGPRs: with AGPR accumulators every VALU touch of O
+    # (the softmax rescale) costs a v_accvgpr_read/write round trip per register.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
 ]
 

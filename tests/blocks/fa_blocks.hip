@@ -109,6 +109,31 @@ __global__ void k_lds_dma(const uint16_t* src, const int* src_chunk, uint16_t* o
     for (int i = l; i < 512; i += 64) out[i] = lh[i];
 }
 
+// lds_dma16_buf: as k_lds_dma through a buffer resource covering the first `bytes` bytes of
+// src; lanes whose chunk starts at or past `bytes` must write zeros. The LDS image is first
+// filled with 0xFFFF (NaN) so that a skipped write would show.
+__global__ void k_lds_dma_buf(const uint16_t* src, const int* src_chunk, int bytes,
+                              uint16_t* out) {
+    __shared__ __attribute__((aligned(1024))) uint16_t lds[512];
+    const int l = threadIdx.x;
+    for (int i = l; i < 512; i += 64) lds[i] = 0xFFFF;
+    __syncthreads();
+    const auto rsrc = make_rsrc(src, bytes);
+    lds_dma16_buf(rsrc, 16 * src_chunk[l], reinterpret_cast<char*>(lds));
+    wait_vmem();
+    __syncthreads();
+    for (int i = l; i < 512; i += 64) out[i] = lds[i];
+}
+
+// sum8_f16: fp32 sum of the eight fp16 values of each 8-element group of x.
+__global__ void k_sum8(const uint16_t* x, float* y, int groups) {
+    for (int gi = threadIdx.x; gi < groups; gi += 64) {
+        f16x8 v;
+        for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(f16, x[8 * gi + e]);
+        y[gi] = sum8_f16(v, 0.0F);
+    }
+}
+
 template <class T>
 struct DevBuf {
     T* p = nullptr;
@@ -229,6 +254,36 @@ int fab_lds_dma(const uint16_t* src, const int* src_chunk, uint16_t* out) {
     FAB_TRY(hipGetLastError());
     FAB_TRY(hipDeviceSynchronize());
     return to_host(out, dout, 512);
+}
+
+int fab_lds_dma_buf(const uint16_t* src, const int* src_chunk, int bytes, uint16_t* out) {
+    for (int i = 0; i < 64; ++i)
+        if (src_chunk[i] < 0 || src_chunk[i] >= 128) return static_cast<int>(hipErrorInvalidValue);
+    if (bytes < 0 || bytes > 1024) return static_cast<int>(hipErrorInvalidValue);
+    // 4 KiB allocation: even a lane the range check failed to stop would stay inside it.
+    DevBuf<uint16_t> ds(2048), dout(512);
+    DevBuf<int> dc(64);
+    FAB_TRY(ds.err);
+    FAB_TRY(hipMemset(ds.p, 0x7F, 2048 * sizeof(uint16_t)));
+    FAB_TRY(to_dev(ds, src, 512));
+    FAB_TRY(to_dev(dc, src_chunk, 64));
+    FAB_TRY(dout.err);
+    hipLaunchKernelGGL(k_lds_dma_buf, dim3(1), dim3(64), 0, 0, ds.p, dc.p, bytes, dout.p);
+    FAB_TRY(hipGetLastError());
+    FAB_TRY(hipDeviceSynchronize());
+    return to_host(out, dout, 512);
+}
+
+int fab_sum8(const uint16_t* x, float* y, int groups) {
+    if (groups <= 0) return static_cast<int>(hipErrorInvalidValue);
+    DevBuf<uint16_t> dx(8 * groups);
+    DevBuf<float> dy(groups);
+    FAB_TRY(to_dev(dx, x, 8 * static_cast<size_t>(groups)));
+    FAB_TRY(dy.err);
+    hipLaunchKernelGGL(k_sum8, dim3(1), dim3(64), 0, 0, dx.p, dy.p, groups);
+    FAB_TRY(hipGetLastError());
+    FAB_TRY(hipDeviceSynchronize());
+    return to_host(y, dy, groups);
 }
 
 }  // extern "C"

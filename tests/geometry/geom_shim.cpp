@@ -5,8 +5,10 @@
 namespace g = fa::geom;
 
 extern "C" {
-int geom_row_xor(int row) { return g::row_xor(row); }
-int geom_swizzle_chunk(int row, int chunk) { return g::swizzle_chunk(row, chunk); }
+int geom_row_xor(int row, int row_bytes) { return g::row_xor(row, row_bytes); }
+int geom_swizzle_chunk(int row, int chunk, int row_bytes) {
+    return g::swizzle_chunk(row, chunk, row_bytes);
+}
 int geom_tile_offset(int row, int chunk, int row_bytes) { return g::tile_offset(row, chunk, row_bytes); }
 int geom_mfma32_c_row(int lane, int r) { return g::mfma32_c_row(lane, r); }
 int geom_mfma32_c_col(int lane) { return g::mfma32_c_col(lane); }
@@ -24,6 +26,12 @@ int geom_tile_needs_mask(int n, int kt, int block_k, int qw, int causal) {
 }
 int geom_tile_fully_masked(int kt, int qw, int rows, int causal) {
     return g::tile_fully_masked(kt, qw, rows, causal != 0) ? 1 : 0;
+}
+int geom_wave_active_tiles(int n, int qw, int rows, int block_k, int n_tiles, int causal) {
+    return g::wave_active_tiles(n, qw, rows, block_k, n_tiles, causal != 0);
+}
+int geom_wave_unmasked_tiles(int n, int qw, int block_k, int n_act, int causal) {
+    return g::wave_unmasked_tiles(n, qw, block_k, n_act, causal != 0);
 }
 void geom_work_of(int block_id, int bh_count, int n_qblocks, int causal, int* bh, int* qb) {
     const g::Work w = g::work_of(block_id, bh_count, n_qblocks, causal != 0);

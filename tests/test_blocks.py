@@ -121,3 +121,29 @@ def test_lds_dma_slot_per_lane(blk):
     _ok(blk.fab_lds_dma(_ptr(src), _ptr(perm), _ptr(out)))
     want = src.reshape(64, 8)[perm].reshape(-1)
     np.testing.assert_array_equal(out, want)
+
+
+def test_buffer_lds_dma_zero_fills_out_of_range(blk):
+    """Lanes whose 16-byte chunk lies at or past the resource size write zeros to LDS (the
+    kernel relies on this for K/V rows >= N); in-range lanes copy their chunk. Offsets up to
+    2 KiB past a 1 KiB source stay inside the range check, so nothing is read out of bounds."""
+    src = (np.arange(512) + 1).astype(np.uint16)
+    perm = np.random.default_rng(7).permutation(64).astype(np.int32)
+    chunks = np.where(np.arange(64) % 3 == 0, perm + 64, perm).astype(np.int32)  # some >= 64
+    for nbytes in (1024, 512, 0):
+        out = np.zeros(512, dtype=np.uint16)
+        _ok(blk.fab_lds_dma_buf(_ptr(src), _ptr(chunks), ctypes.c_int(nbytes), _ptr(out)))
+        got = out.reshape(64, 8)
+        for lane in range(64):
+            c = chunks[lane]
+            want = src.reshape(64, 8)[c] if 16 * c + 16 <= nbytes else np.zeros(8, np.uint16)
+            np.testing.assert_array_equal(got[lane], want, err_msg=f"lane {lane} bytes {nbytes}")
+
+
+def test_sum8_f16_accumulates_in_fp32(blk):
+    rng = np.random.default_rng(8)
+    x = rng.uniform(0, 256, size=(1000, 8)).astype(np.float16)
+    y = np.zeros(1000, dtype=np.float32)
+    _ok(blk.fab_sum8(_ptr(x.view(np.uint16)), _ptr(y), ctypes.c_int(1000)))
+    want = x.astype(np.float64).sum(axis=1)
+    np.testing.assert_allclose(y, want, rtol=2e-7 * 8, atol=0)

@@ -4,9 +4,11 @@ same header. Counterpart of the reference's host-side swizzle checks
 gfx950 access patterns, plus the tile-count, mask and work-map arithmetic
 (csrc/kernels/flash_fwd.cu:183-194, 502-505).
 
-LDS bank model used here: 32 banks of 4 bytes (bank = byte_offset / 4 mod 32); a
-ds_read_b128 serves 8 lanes (128 bytes) per cycle and a ds_read_b64_tr_b16 one 16-lane group
-per cycle. An access group is conflict-free when it touches each bank exactly once.
+LDS bank model used here, measured on MI355X with a saturating microbenchmark of
+ds_read_b128 / ds_read_b64_tr_b16 over fixed lane-offset patterns (the patterns and their
+measured outcome are the table MEASURED below): 64 banks of 4 bytes (bank = byte_offset / 4
+mod 64); a ds_read_b128 is served 16 lanes at a time, a ds_read_b64_tr_b16 32 lanes at a time;
+a group is conflict-free when no bank is hit at two different addresses.
 """
 
 from __future__ import annotations
@@ -28,27 +30,77 @@ def geo():
 
 
 def _banks(byte_off, nbytes):
-    return [((byte_off + 4 * w) // 4) % 32 for w in range(nbytes // 4)]
+    return [((byte_off + 4 * w) // 4) % 64 for w in range(nbytes // 4)]
+
+
+def _conflict_free(offsets, nbytes, group):
+    """True when every `group`-lane group hits each bank at no more than one address."""
+    for g0 in range(0, len(offsets), group):
+        seen = {}
+        for o in offsets[g0:g0 + group]:
+            for w in range(nbytes // 4):
+                addr = o + 4 * w
+                bank = (addr // 4) % 64
+                if seen.setdefault(bank, addr) != addr:
+                    return False
+    return True
+
+
+def _k_offsets(geo, d, nb=0, kk=0):
+    rb = 2 * d
+    return [geo.geom_tile_offset(32 * nb + (l % 32), 2 * kk + l // 32, rb) for l in range(64)]
+
+
+# Patterns timed on MI355X (16 waves of one workgroup, 8 reads in flight each): True = ran at
+# the conflict-free rate (same time as a contiguous read), False = measurably slower.
+MEASURED_B128 = {
+    "contiguous": ([16 * l for l in range(64)], True),
+    "broadcast": ([0] * 64, True),
+    "stride256": ([256 * l for l in range(32)] * 2, False),
+    "16x16B per 256B row": ([16 * (l % 16) + 256 * (l // 16) for l in range(64)], True),
+    "8x16B per 256B row": ([16 * (l % 8) + 256 * (l // 8) for l in range(64)], False),
+    "8x16B per 128B row": ([16 * (l % 8) + 128 * (l // 8) for l in range(64)], True),
+    "d128 rows, no swizzle": ([256 * (l % 32) + 16 * (l // 32) for l in range(64)], False),
+    "d128 rows, 3-bit row xor": ([256 * (l % 32) + 16 * ((l // 32) ^ (((l % 32) & 3) << 1 | ((l % 32) >> 2) & 1)) for l in range(64)], False),
+    "d64 rows, no swizzle": ([128 * (l % 32) + 16 * (l // 32) for l in range(64)], False),
+}
+MEASURED_TR = {
+    "contiguous": ([8 * l for l in range(64)], True),
+    "32x8B per 256B": ([8 * (l % 32) + 512 * (l // 32) for l in range(64)], True),
+    "16x8B per 256B row": ([8 * (l % 16) + 256 * (l // 16) for l in range(64)], False),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MEASURED_B128))
+def test_bank_model_matches_measured_b128(name):
+    offs, free = MEASURED_B128[name]
+    assert _conflict_free(offs, 16, 16) == free
+
+
+@pytest.mark.parametrize("name", sorted(MEASURED_TR))
+def test_bank_model_matches_measured_tr(name):
+    offs, free = MEASURED_TR[name]
+    assert _conflict_free(offs, 8, 32) == free
 
 
 @pytest.mark.parametrize("d", [64, 128])
 def test_swizzle_is_a_permutation_of_each_row(geo, d):
     cpr = d // 8
     for row in range(256):
-        phys = [geo.geom_swizzle_chunk(row, c) for c in range(cpr)]
+        phys = [geo.geom_swizzle_chunk(row, c, 2 * d) for c in range(cpr)]
         assert sorted(phys) == list(range(cpr))
-        assert all(geo.geom_swizzle_chunk(row, p) == c for c, p in enumerate(phys))  # involution
+        assert all(geo.geom_swizzle_chunk(row, p, 2 * d) == c for c, p in enumerate(phys))
 
 
 @pytest.mark.parametrize("d", [64, 128])
 def test_k_fragment_reads_are_conflict_free(geo, d):
     """ds_read_b128 of the S^T A operand: lane l reads row 32*nb + l%32, chunk 2*kk + l//32."""
-    rb = 2 * d
-    for nb, kk in itertools.product(range(2), range(d // 16)):
-        offs = [geo.geom_tile_offset(32 * nb + (l % 32), 2 * kk + l // 32, rb) for l in range(64)]
-        for g0 in range(0, 64, 8):
-            banks = sum((_banks(o, 16) for o in offs[g0:g0 + 8]), [])
-            assert sorted(banks) == list(range(32)), (nb, kk, g0)
+    for nb, kk in itertools.product(range(4), range(d // 16)):
+        offs = _k_offsets(geo, d, nb, kk)
+        assert _conflict_free(offs, 16, 16), (nb, kk)
+        for g0 in range(0, 64, 16):  # and each group spreads over all 64 banks
+            banks = sum((_banks(o, 16) for o in offs[g0:g0 + 16]), [])
+            assert sorted(banks) == list(range(64)), (nb, kk, g0)
 
 
 def _v_read_offsets(geo, d, nb, h, db, e):
@@ -60,6 +112,9 @@ def _v_read_offsets(geo, d, nb, h, db, e):
         row = 32 * nb + 16 * h + 8 * e + 4 * hi + geo.geom_tr16_row(l)
         colh = 32 * db + 16 * ((l >> 4) & 1) + geo.geom_tr16_col(l)
         out.append(geo.geom_tile_offset(row, colh // 8, rb) + 2 * (colh % 8))
+        # the kernel adds the 16-row multiples as immediates to an offset computed at row % 16
+        local = geo.geom_tile_offset(row % 16, colh // 8, rb) + 2 * (colh % 8)
+        assert out[-1] == local + (row - row % 16) * rb
     return out
 
 
@@ -67,9 +122,10 @@ def _v_read_offsets(geo, d, nb, h, db, e):
 def test_v_transposed_reads_are_conflict_free(geo, d):
     for nb, h, db, e in itertools.product(range(2), range(2), range(d // 32), range(2)):
         offs = _v_read_offsets(geo, d, nb, h, db, e)
-        for g0 in range(0, 64, 16):
-            banks = sum((_banks(o, 8) for o in offs[g0:g0 + 16]), [])
-            assert sorted(banks) == list(range(32)), (nb, h, db, e, g0)
+        assert _conflict_free(offs, 8, 32), (nb, h, db, e)
+        for g0 in range(0, 64, 32):
+            banks = sum((_banks(o, 8) for o in offs[g0:g0 + 32]), [])
+            assert sorted(banks) == list(range(64)), (nb, h, db, e, g0)
 
 
 @pytest.mark.parametrize("d", [64, 128])
@@ -85,7 +141,7 @@ def test_v_transposed_reads_deliver_the_pv_keys(geo, d):
             for l in range(g0, g0 + 16):
                 row = offs[l] // rb
                 phys_chunk = (offs[l] % rb) // 16
-                colh = 8 * geo.geom_swizzle_chunk(row, phys_chunk) + (offs[l] % 16) // 2
+                colh = 8 * geo.geom_swizzle_chunk(row, phys_chunk, rb) + (offs[l] % 16) // 2
                 cells.append((row, colh))
             rows = sorted({r for r, _ in cells})
             assert len(rows) == 4 and rows == list(range(rows[0], rows[0] + 4))
@@ -97,6 +153,15 @@ def test_v_transposed_reads_deliver_the_pv_keys(geo, d):
                 assert cols[0] + j == 32 * db + (lane % 32)
                 for i in range(4):
                     assert rows[i] == 32 * nb + 16 * h + geo.geom_pv_key(lane, 4 * e + i)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_k_fragment_immediates(geo, d):
+    """The kernel reads K fragment (nb, kk) at koff[kk] + 32*nb*row_bytes."""
+    rb = 2 * d
+    for nb, kk, l in itertools.product(range(4), range(d // 16), range(64)):
+        assert geo.geom_tile_offset(32 * nb + l % 32, 2 * kk + l // 32, rb) == \
+            geo.geom_tile_offset(l % 32, 2 * kk + l // 32, rb) + 32 * nb * rb
 
 
 def test_p_operand_slots_are_the_score_accumulators(geo):
