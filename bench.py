@@ -85,6 +85,21 @@ def cpu_baseline(cfg, q, k, v, budget_s: float) -> dict:
     }
 
 
+def copy_calibration(nbytes: int, steps: int) -> int:
+    """Copies nbytes device-to-device `steps` times (torch copy_ kernel): each launch reads and
+    writes exactly nbytes, which calibrates the HBM byte counters of rocprofv3."""
+    import torch
+
+    src = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": nbytes,
+                      "bytes_written": nbytes, "launches": steps}), flush=True)
+    return 0
+
+
 def traffic_from_profiles(cfg_name: str, causal: bool):
     """HBM bytes per launch measured with rocprofv3 PMC counters, if a summary was committed."""
     f = REPO / "profiles" / f"traffic_{cfg_name}.json"
@@ -106,6 +121,9 @@ def main() -> int:
     ap.add_argument("--variant", default="opt", choices=["baseline", "opt", "fp16acc"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="calibration only: time a plain device copy of this many bytes (the "
+                         "reference workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -124,6 +142,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
+    if args.copy_bytes:
+        return copy_calibration(args.copy_bytes, args.steps)
     cfg = CONFIGS[args.config]
     modes = list(cfg.causal)
     q, k, v = make_inputs(cfg)

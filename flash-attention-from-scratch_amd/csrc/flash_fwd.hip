@@ -47,6 +47,13 @@ namespace g = fa::geom;
 
 // Compile-time tile shape and options. Counterpart of the reference's Config/Opt pair
 // (csrc/kernels/flash_fwd.cu:70-100), re-derived for 64-wide waves and 32x32 MFMA blocks.
+#ifndef FA_PINGPONG
+#define FA_PINGPONG 0
+#endif
+#ifndef FA_OPTIMISTIC
+#define FA_OPTIMISTIC 1
+#endif
+
 template <int D_, int BC_, int NW_, bool LAZY_, bool PIPE_>
 struct Tile {
     static constexpr int D = D_;            // head dim (64 or 128)
@@ -54,6 +61,8 @@ struct Tile {
     static constexpr int NW = NW_;          // wave64s per workgroup
     static constexpr bool LAZY = LAZY_;     // rescale O only when a row max grows by > 2^8
     static constexpr bool PIPE = PIPE_;     // software-pipelined schedule (QK of j+1 || softmax j)
+    // Two waves per SIMD run the pipelined iteration half a step apart (needs NW = 8).
+    static constexpr bool PINGPONG = PIPE_ && NW_ == 8 && FA_PINGPONG;
     static constexpr int BR = 32 * NW;      // query rows per workgroup
     static constexpr int THREADS = 64 * NW;
     static constexpr int ROW_BYTES = 2 * D;
@@ -352,7 +361,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
 // Scheduler pattern: N times {one MFMA, then up to VALU_PER VALU instructions}. Masks of
 // __builtin_amdgcn_sched_group_barrier (LLVM AMDGPU): 0x008 MFMA, 0x002 VALU.
 #ifndef FA_VALU_PER_MFMA
-#define FA_VALU_PER_MFMA 10
+#define FA_VALU_PER_MFMA 8
 #endif
 template <int VALU_PER, int... I>
 __device__ __forceinline__ void sched_mfma_valu(std::integer_sequence<int, I...>) {
@@ -361,15 +370,16 @@ __device__ __forceinline__ void sched_mfma_valu(std::integer_sequence<int, I...>
      ...);
 }
 
-// Region pattern of the steady-state iteration: the K fragment reads, two {MFMA, VALU}
-// stages, then the V^T fragment reads and the DMA refill (0x100 DS read, 0x020 VMEM read),
-// then the remaining stages. The K reads come first so the first MFMA waits for them only.
+// Region pattern of the steady-state iteration: the DMA refill (0x020 VMEM read) and the K
+// fragment reads (0x100 DS read) first, two {MFMA, VALU} stages, then the V^T fragment reads,
+// then the remaining stages. The K reads come before the V reads so the first MFMA waits for
+// its own operand only.
 template <int VALU_PER, int NK, int NV, int NDMA, int M>
 __device__ __forceinline__ void sched_steady_region() {
+    __builtin_amdgcn_sched_group_barrier(0x020, NDMA, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, NK, 0);
     sched_mfma_valu<VALU_PER>(std::make_integer_sequence<int, 2>{});
     __builtin_amdgcn_sched_group_barrier(0x100, NV, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, NDMA, 0);
     sched_mfma_valu<VALU_PER>(std::make_integer_sequence<int, M - 2>{});
 }
 
@@ -434,6 +444,52 @@ __device__ __forceinline__ void qk_softmax_interleaved(
     asm volatile("" ::"v"(l_run));
 }
 
+// ---- QK of tile j+1 interleaved with an optimistic softmax of tile j --------------------------
+// The common case of the steady state needs no row max: with the running max m kept from the
+// last rescale, p = exp2(s*c - m) is computed directly and packed to fp16. If some p of the
+// wave reaches 65520 (its score exceeds m by 16 log2 units or more, including the first tile,
+// where m = -inf) the fp16 pack gives inf and so does the lane's fp32 row sum; then
+// `overflow` is set (wave-uniform) and the caller redoes the tile with the exact softmax,
+// which updates m and rescales O. Otherwise every p lies in [0, 65504], which fp16 holds
+// with its usual 11-bit precision and the fp32 accumulators of O and l hold easily, so the
+// result is the same softmax with a different (valid) reference point m. Stage m issues MFMA m
+// of S^T_{j+1} and a slice of the exponentials; the caller's sched_group_barrier pattern
+// interleaves them.
+template <class T>
+__device__ __forceinline__ void qk_softmax_optimistic(
+    const f16x8 (&kf)[T::NB][T::KK], const f16x8 (&qf)[T::KK], const f32x16 (&s)[T::NB],
+    float scale_log2, float m_run, float& l_run, bool& overflow, f32x16 (&s_next)[T::NB],
+    f16x8 (&p)[T::NB][2]) {
+    constexpr int M = T::NB * T::KK;  // MFMA stages
+    constexpr int E = 16 * T::NB;     // scores per lane
+    constexpr int PER_EXP = (E + M - 1) / M;
+    float pe[E];
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) s_next[nb] = f32x16{};
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        s_next[m / T::KK] = mfma32(kf[m / T::KK][m % T::KK], qf[m % T::KK], s_next[m / T::KK]);
+#pragma unroll
+        for (int e = m * PER_EXP; e < (m + 1) * PER_EXP && e < E; ++e)
+            pe[e] = exp2_fast(fmaf(s[e / 16][e % 16], scale_log2, -m_run));
+    }
+    float sum = 0.0F;
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) {
+        const float* e = pe + 16 * nb;
+        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
+        sum = sum8_f16(p[nb][1], sum8_f16(p[nb][0], sum));
+    }
+    overflow = wave_any(!(sum < INFINITY));
+    if (!overflow) l_run += sum;
+    // Empty asm that reads P and l: keeps their computation in this block (see
+    // qk_softmax_interleaved).
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) asm volatile("" ::"v"(p[nb][0]), "v"(p[nb][1]));
+    asm volatile("" ::"v"(l_run));
+}
+
 // ---- kernel, software-pipelined schedule (the "opt" build) ----------------------------------
 // Each wave overlaps the S^T = K Q^T MFMAs of tile j+1 with the softmax VALU work of tile j in
 // one straight-line block, then issues tile j's P.V MFMAs; with two waves per SIMD the matrix
@@ -447,7 +503,13 @@ template <class T, bool CAUSAL>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, int n, int bh_count, int n_qblocks, float scale_log2, int negate_q) {
-    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+    // Four separate LDS objects (K and V, two buffers each): with the buffer known at compile
+    // time, the compiler can tell that a DMA refill and a fragment read touch different
+    // objects and adds no wait between them.
+    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -464,8 +526,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
     const int n_plain = g::wave_unmasked_tiles(n, qw, T::BC, n_act, CAUSAL);
 
-    auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
-    auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
+    auto kbuf = [&](int b) { return b ? k_lds1 : k_lds0; };
+    auto vbuf = [&](int b) { return b ? v_lds1 : v_lds0; };
 
     const TileDma<T> dma(wave, lane);
     load_tile<T>(kh, 0, n, kbuf(0), dma);
@@ -487,13 +549,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     f32x16 s2[T::NB];
     if (n_act > 0) qk_tile<T>(kbuf(0), fr, qf, s);
 
-    // Steady state: tile j unmasked, tile j+1 active. The LDS reads of the iteration (K
-    // fragments of tile j+1, V^T fragments of tile j) precede the DMA refill in program order:
-    // the compiler cannot tell that the refill writes the other buffers and would otherwise
-    // make the transposed reads wait for it. The refill (K_{j+2} into K buffer j%2, V_{j+1}
-    // into V buffer (j+1)%2; both buffers were last read before this iteration's barrier) is
-    // unconditional so it shares the scheduling region; a K tile past the end reads as zeros
-    // into a buffer nobody reads again. The QK MFMAs of tile j+1 are interleaved with tile j's
+    // Steady state: tile j unmasked, tile j+1 active. Right after the barrier the refill is
+    // requested (K_{j+2} into K buffer j%2, V_{j+1} into V buffer (j+1)%2; both buffers were
+    // last read before this barrier), so it has a whole iteration to land; it is
+    // unconditional so it shares the scheduling region, and a K tile past the end reads as
+    // zeros into a buffer nobody reads again. The fragment reads of this iteration (K of tile
+    // j+1, V^T of tile j) touch the other LDS objects, so they need not wait for it. The QK MFMAs of tile j+1 are interleaved with tile j's
     // softmax (sched_steady_region); then, after the rarely taken rescale branch, tile j's PV
     // MFMAs. Two tiles per trip, so every buffer address is an immediate and the score
     // registers alternate between s and s2 without copies.
@@ -501,33 +562,90 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
         constexpr int PAR = decltype(parity)::value;  // jj % 2
         wait_vmem();
         __syncthreads();
+        load_tile<T>(kh, (jj + 2) * T::BC, n, kbuf(PAR), dma);
+        load_tile<T>(vh, (jj + 1) * T::BC, n, vbuf(1 - PAR), dma);
         f16x8 kf[T::NB][T::KK];
         load_k_frags<T>(kbuf(1 - PAR), fr, kf);
         f16x8 vf[T::NB][2][T::DB];
         load_v_frags<T>(vbuf(PAR), fr, vf);
-        load_tile<T>(kh, (jj + 2) * T::BC, n, kbuf(PAR), dma);
-        load_tile<T>(vh, (jj + 1) * T::BC, n, vbuf(1 - PAR), dma);
         f16x8 p[T::NB][2];
         float alpha;
         bool rescale;
+        if constexpr (T::LAZY && FA_OPTIMISTIC) {
+            bool overflow;
+            qk_softmax_optimistic<T>(kf, qf, s_cur, scale_log2, m_run, l_run, overflow, s_nxt,
+                                     p);
+            sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
+                                2 * T::DMA_ITERS, T::NB * T::KK>();
+            if (overflow) {  // rare: the exact softmax of this tile, new max, rescaled O
+                softmax_tile<T>(s_cur, scale_log2, m_run, l_run, alpha, rescale, p);
+                if (rescale) rescale_o<T>(oacc, alpha);
+            }
+        } else {
+            qk_softmax_interleaved<T>(kf, qf, s_cur, scale_log2, m_run, l_run, alpha, rescale,
+                                      s_nxt, p);
+            sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
+                                2 * T::DMA_ITERS, T::NB * T::KK>();
+            if (rescale) rescale_o<T>(oacc, alpha);
+        }
+        pv_frags<T>(vf, p, oacc);
+    };
+    // Ping-pong variant (waves NW/2..NW-1 when PINGPONG): the same work rotated by half an
+    // iteration. Such a wave starts iteration j with the PV MFMAs of tile j-1 (P and V^T
+    // fragments kept in registers from the previous iteration), then runs the QK MFMAs of tile
+    // j+1 with tile j's softmax; O is rescaled after PV_{j-1} and before PV_j, as required.
+    // The waves of a workgroup are dealt round-robin to the four SIMDs, so each SIMD holds one
+    // wave of each half: while one is in its VALU-heavy softmax phase the other feeds the
+    // matrix pipe with PV MFMAs, and the other way round.
+    f16x8 p_prev[T::NB][2];
+    f16x8 vf_prev[T::NB][2][T::DB];
+    bool pending = false;
+    auto steady_rot = [&](int jj, auto parity, f32x16(&s_cur)[T::NB], f32x16(&s_nxt)[T::NB]) {
+        constexpr int PAR = decltype(parity)::value;  // jj % 2
+        wait_vmem();
+        __syncthreads();
+        load_tile<T>(kh, (jj + 2) * T::BC, n, kbuf(PAR), dma);
+        load_tile<T>(vh, (jj + 1) * T::BC, n, vbuf(1 - PAR), dma);
+        if (pending) pv_frags<T>(vf_prev, p_prev, oacc);
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 kf[T::NB][T::KK];
+        load_k_frags<T>(kbuf(1 - PAR), fr, kf);
+        load_v_frags<T>(vbuf(PAR), fr, vf_prev);
+        float alpha;
+        bool rescale;
         qk_softmax_interleaved<T>(kf, qf, s_cur, scale_log2, m_run, l_run, alpha, rescale, s_nxt,
-                                  p);
+                                  p_prev);
         sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
                             2 * T::DMA_ITERS, T::NB * T::KK>();
         if (rescale) rescale_o<T>(oacc, alpha);
-        pv_frags<T>(vf, p, oacc);
+        pending = true;
     };
+    const bool rotated = T::PINGPONG && wave >= T::NW / 2;
     const int n_steady = min(n_plain, n_act - 1);
     int j = 0;
-    for (; j + 2 <= n_steady; j += 2) {
-        steady(j, std::integral_constant<int, 0>{}, s, s2);
-        steady(j + 1, std::integral_constant<int, 1>{}, s2, s);
-    }
-    if (j < n_steady) {
-        steady(j, std::integral_constant<int, 0>{}, s, s2);
+    if (rotated) {
+        for (; j + 2 <= n_steady; j += 2) {
+            steady_rot(j, std::integral_constant<int, 0>{}, s, s2);
+            steady_rot(j + 1, std::integral_constant<int, 1>{}, s2, s);
+        }
+        if (j < n_steady) {
+            steady_rot(j, std::integral_constant<int, 0>{}, s, s2);
 #pragma unroll
-        for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
-        ++j;
+            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+            ++j;
+        }
+        if (pending) pv_frags<T>(vf_prev, p_prev, oacc);
+    } else {
+        for (; j + 2 <= n_steady; j += 2) {
+            steady(j, std::integral_constant<int, 0>{}, s, s2);
+            steady(j + 1, std::integral_constant<int, 1>{}, s2, s);
+        }
+        if (j < n_steady) {
+            steady(j, std::integral_constant<int, 0>{}, s, s2);
+#pragma unroll
+            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+            ++j;
+        }
     }
 
     // General tiles (diagonal, tail, or only waited through); same read-then-refill order.
@@ -579,10 +697,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
 #define FA_BASE_D128 64, 4, false, false
 #endif
 #ifndef FA_OPT_D64
-#define FA_OPT_D64 64, 4, true, true
+#define FA_OPT_D64 32, 4, true, true
 #endif
 #ifndef FA_OPT_D64_CAUSAL
-#define FA_OPT_D64_CAUSAL 64, 4, true, true
+#define FA_OPT_D64_CAUSAL 32, 4, true, true
 #endif
 #ifndef FA_OPT_D128
 #define FA_OPT_D128 32, 8, true, true

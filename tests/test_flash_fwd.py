@@ -76,6 +76,25 @@ def test_large_logits_are_stable(causal, variant):
 
 
 @pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_row_max_jumps_mid_sequence(d, causal):
+    """Scores that stay small for 1024 keys and then jump by far more than 2^16 in the middle
+    of the key loop: the running max must be raised (and O rescaled) inside the steady-state
+    loop, not only on the first tile."""
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(1, 2, 2048, d, generator=g)
+    k = torch.randn(1, 2, 2048, d, generator=g)
+    k[:, :, :1024] *= 0.05
+    k[:, :, 1024:] *= 3.0
+    v = torch.randn(1, 2, 2048, d, generator=g)
+    q, k, v = (t.half().cuda() for t in (q, k, v))
+    for variant in VARIANTS:
+        out = _fa().forward_variant(q, k, v, causal=causal, variant=variant)
+        assert torch.isfinite(out).all()
+        _close(out, orc.attention_fp32(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_uniform_scores(d, variant):
     """q = 0: every p = 1, O = mean(V) (tests/test_flash_fwd.py:60-70), a closed form."""
