@@ -115,8 +115,9 @@ def traffic_from_profiles(cfg_name: str, causal: bool):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=30)
+    # The GPU takes tens of milliseconds to ramp its clock from idle: warm up past that.
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg4")
     ap.add_argument("--variant", default="opt", choices=["baseline", "opt", "fp16acc"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

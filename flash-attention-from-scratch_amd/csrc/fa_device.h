@@ -56,8 +56,10 @@ __device__ __forceinline__ void lds_dma16(const void* global_src, char* lds_wave
 // Buffer resource for raw (stride 0) buffer loads of `bytes` bytes from `base`; the hardware
 // range check returns zeros for any access at or past `bytes` (4th descriptor dword of gfx9
 // parts: 0x00020000, 32-bit data format).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+// `bytes` is the 32-bit num_records field, unsigned: a range of up to 2^32 - 1 bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                             __builtin_bit_cast(int, bytes), 0x00020000);
 }
 
 // 16-byte buffer -> LDS copy (buffer_load_dwordx4 ... lds): lane i reads rsrc + voffset and

@@ -7,8 +7,8 @@
 //     each wave owns 32 of them for the whole kernel, so a row's softmax statistics never leave
 //     the wave (the FA2 split-Q scheme of csrc/kernels/flash_fwd.cu:7-12).
 //   * The workgroup streams over keys in tiles of BC rows, double-buffered in LDS and filled by
-//     global_load_lds_dwordx4 (direct HBM/L2 -> LDS, no VGPR staging): tile j+1 is in flight
-//     while tile j is computed, with one workgroup barrier per tile.
+//     buffer_load_dwordx4 ... lds (direct HBM/L2 -> LDS, no VGPR staging): the next tiles are
+//     in flight while tile j is computed, with one workgroup barrier per tile.
 //
 // Per tile and wave, on CDNA4 matrix cores:
 //   * S^T = K Q^T with v_mfma_f32_32x32x16_f16: A = K rows (read from swizzled LDS with
@@ -23,8 +23,9 @@
 //     feature column.
 //   * Causal: tiles right of the diagonal are never loaded; masking runs only on diagonal and
 //     tail tiles; longest query blocks launch first.
-//   * Ragged N: K/V/Q row indices are clamped to N-1 (always in bounds); clamped keys are
-//     masked to -inf and so contribute exactly 0, clamped query rows are never stored.
+//   * Ragged N: the buffer resource of a K/V tile ends at row N, so rows >= N arrive as zeros
+//     (their scores are masked to -inf and contribute exactly 0); Q row indices are clamped to
+//     N-1 and the clamped rows are never stored.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -107,7 +108,7 @@ template <class T>
 __device__ __forceinline__ void load_tile(const f16* head, int kt, int n, char* lds,
                                           const TileDma<T>& dma) {
     const char* base = reinterpret_cast<const char*>(head) + static_cast<size_t>(kt) * T::ROW_BYTES;
-    const auto rsrc = make_rsrc(base, max(0, n - kt) * T::ROW_BYTES);
+    const auto rsrc = make_rsrc(base, static_cast<unsigned>(max(0, n - kt)) * T::ROW_BYTES);
 #pragma unroll
     for (int it = 0; it < T::DMA_ITERS; ++it) lds_dma16_buf(rsrc, dma.voff[it], lds + dma.lds0[it]);
 }
