@@ -48,28 +48,29 @@ namespace g = fa::geom;
 
 // Compile-time tile shape and options. Counterpart of the reference's Config/Opt pair
 // (csrc/kernels/flash_fwd.cu:70-100), re-derived for 64-wide waves and 32x32 MFMA blocks.
-#ifndef FA_PINGPONG
-#define FA_PINGPONG 0
-#endif
 #ifndef FA_OPTIMISTIC
 #define FA_OPTIMISTIC 1
 #endif
 
-template <int D_, int BC_, int NW_, bool LAZY_, bool PIPE_>
+// Main-loop schedules: SIMPLE (flash_fwd_kernel), PIPE (flash_fwd_pipelined: QK of tile j+1
+// interleaved with the softmax of tile j in each wave), PINGPONG (flash_fwd_pingpong: two
+// groups of waves alternate between an MFMA-only phase and a softmax phase).
+enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2 };
+
+template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
     static constexpr int D = D_;            // head dim (64 or 128)
     static constexpr int BC = BC_;          // keys per K/V tile
     static constexpr int NW = NW_;          // wave64s per workgroup
     static constexpr bool LAZY = LAZY_;     // rescale O only when a row max grows by > 2^8
-    static constexpr bool PIPE = PIPE_;     // software-pipelined schedule (QK of j+1 || softmax j)
-    // Two waves per SIMD run the pipelined iteration half a step apart (needs NW = 8).
-    static constexpr bool PINGPONG = PIPE_ && NW_ == 8 && FA_PINGPONG;
+    static constexpr int SCHED = SCHED_;    // main-loop schedule (Sched)
     static constexpr int BR = 32 * NW;      // query rows per workgroup
     static constexpr int THREADS = 64 * NW;
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
-    static constexpr int LDS_BYTES = 4 * TILE_BYTES;   // {K, V} x 2 buffers
+    static constexpr int NBUF = SCHED == PINGPONG ? 3 : 2;  // buffers each for K and V
+    static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
     static constexpr int DB = D / 32;                  // 32-wide output blocks over D
@@ -491,7 +492,56 @@ __device__ __forceinline__ void qk_softmax_optimistic(
     asm volatile("" ::"v"(l_run));
 }
 
-// ---- kernel, software-pipelined schedule (the "opt" build) ----------------------------------
+// ---- tiles outside the steady state ----------------------------------------------------------
+// Tiles j0 .. n_tiles-1 of a wave, one workgroup barrier each: diagonal and tail tiles (masked),
+// the last tile, and tiles a causal wave only waits through. K_t and V_t live in buffer t % NBUF.
+// On entry S_j0 is in s and K_{j0+1} and V_{j0} are resident once the outstanding DMA has landed
+// (any DMA still in flight targets other buffers, or carries the same tile). Per tile: wait,
+// barrier, fragment reads of K_{j+1} and V_j, refill of K_{j+2} and V_{j+1} into buffers no wave
+// reads in this iteration, S_{j+1}, mask, exact softmax, P.V.
+template <class T, bool CAUSAL, int NBUF>
+__device__ __forceinline__ void general_tiles(
+    int j, int n_tiles, int n_act, int n, int qw, int qrow, int lane, const f16* kh, const f16* vh,
+    char* const (&kb)[NBUF], char* const (&vb)[NBUF], const TileDma<T>& dma, const Frag<T>& fr,
+    const f16x8 (&qf)[T::KK], f32x16 (&s)[T::NB], f32x16 (&oacc)[T::DB], float scale_log2,
+    float& m_run, float& l_run) {
+    for (; j < n_tiles; ++j) {
+        wait_vmem();
+        __syncthreads();
+        const bool act = j < n_act;
+        const bool act_next = j + 1 < n_act;
+        f16x8 kf[T::NB][T::KK];
+        f16x8 vf[T::NB][2][T::DB];
+        if (act_next) load_k_frags<T>(kb[(j + 1) % NBUF], fr, kf);
+        if (act) load_v_frags<T>(vb[j % NBUF], fr, vf);
+        if (j + 2 < n_tiles) load_tile<T>(kh, (j + 2) * T::BC, n, kb[(j + 2) % NBUF], dma);
+        if (j + 1 < n_tiles) load_tile<T>(vh, (j + 1) * T::BC, n, vb[(j + 1) % NBUF], dma);
+        if (!act) continue;  // wave-uniform: fully masked for this wave (causal)
+        f32x16 s2[T::NB];
+        if (act_next) {
+#pragma unroll
+            for (int nb = 0; nb < T::NB; ++nb) {
+                s2[nb] = f32x16{};
+#pragma unroll
+                for (int kk = 0; kk < T::KK; ++kk) s2[nb] = mfma32(kf[nb][kk], qf[kk], s2[nb]);
+            }
+        }
+        const int kt = j * T::BC;
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
+        f16x8 p[T::NB][2];
+        float alpha;
+        bool rescale;
+        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale_o<T>(oacc, alpha);
+        pv_frags<T>(vf, p, oacc);
+        if (act_next) {
+#pragma unroll
+            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+        }
+    }
+}
+
+// ---- kernel, software-pipelined schedule ----------------------------------
 // Each wave overlaps the S^T = K Q^T MFMAs of tile j+1 with the softmax VALU work of tile j in
 // one straight-line block, then issues tile j's P.V MFMAs; with two waves per SIMD the matrix
 // pipe is fed while either wave is in its softmax. K and V are double-buffered separately:
@@ -591,123 +641,322 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
         }
         pv_frags<T>(vf, p, oacc);
     };
-    // Ping-pong variant (waves NW/2..NW-1 when PINGPONG): the same work rotated by half an
-    // iteration. Such a wave starts iteration j with the PV MFMAs of tile j-1 (P and V^T
-    // fragments kept in registers from the previous iteration), then runs the QK MFMAs of tile
-    // j+1 with tile j's softmax; O is rescaled after PV_{j-1} and before PV_j, as required.
-    // The waves of a workgroup are dealt round-robin to the four SIMDs, so each SIMD holds one
-    // wave of each half: while one is in its VALU-heavy softmax phase the other feeds the
-    // matrix pipe with PV MFMAs, and the other way round.
-    f16x8 p_prev[T::NB][2];
-    f16x8 vf_prev[T::NB][2][T::DB];
-    bool pending = false;
-    auto steady_rot = [&](int jj, auto parity, f32x16(&s_cur)[T::NB], f32x16(&s_nxt)[T::NB]) {
-        constexpr int PAR = decltype(parity)::value;  // jj % 2
-        wait_vmem();
-        __syncthreads();
-        load_tile<T>(kh, (jj + 2) * T::BC, n, kbuf(PAR), dma);
-        load_tile<T>(vh, (jj + 1) * T::BC, n, vbuf(1 - PAR), dma);
-        if (pending) pv_frags<T>(vf_prev, p_prev, oacc);
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 kf[T::NB][T::KK];
-        load_k_frags<T>(kbuf(1 - PAR), fr, kf);
-        load_v_frags<T>(vbuf(PAR), fr, vf_prev);
-        float alpha;
-        bool rescale;
-        qk_softmax_interleaved<T>(kf, qf, s_cur, scale_log2, m_run, l_run, alpha, rescale, s_nxt,
-                                  p_prev);
-        sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
-                            2 * T::DMA_ITERS, T::NB * T::KK>();
-        if (rescale) rescale_o<T>(oacc, alpha);
-        pending = true;
-    };
-    const bool rotated = T::PINGPONG && wave >= T::NW / 2;
     const int n_steady = min(n_plain, n_act - 1);
     int j = 0;
-    if (rotated) {
-        for (; j + 2 <= n_steady; j += 2) {
-            steady_rot(j, std::integral_constant<int, 0>{}, s, s2);
-            steady_rot(j + 1, std::integral_constant<int, 1>{}, s2, s);
-        }
-        if (j < n_steady) {
-            steady_rot(j, std::integral_constant<int, 0>{}, s, s2);
+    for (; j + 2 <= n_steady; j += 2) {
+        steady(j, std::integral_constant<int, 0>{}, s, s2);
+        steady(j + 1, std::integral_constant<int, 1>{}, s2, s);
+    }
+    if (j < n_steady) {
+        steady(j, std::integral_constant<int, 0>{}, s, s2);
 #pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
-            ++j;
-        }
-        if (pending) pv_frags<T>(vf_prev, p_prev, oacc);
-    } else {
-        for (; j + 2 <= n_steady; j += 2) {
-            steady(j, std::integral_constant<int, 0>{}, s, s2);
-            steady(j + 1, std::integral_constant<int, 1>{}, s2, s);
-        }
-        if (j < n_steady) {
-            steady(j, std::integral_constant<int, 0>{}, s, s2);
-#pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
-            ++j;
-        }
+        for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+        ++j;
     }
 
-    // General tiles (diagonal, tail, or only waited through); same read-then-refill order.
-    for (; j < n_tiles; ++j) {
-        wait_vmem();
-        __syncthreads();
-        const bool act = j < n_act;
-        const bool act_next = j + 1 < n_act;
-        f16x8 kf[T::NB][T::KK];
-        f16x8 vf[T::NB][2][T::DB];
-        if (act_next) load_k_frags<T>(kbuf((j + 1) & 1), fr, kf);
-        if (act) load_v_frags<T>(vbuf(j & 1), fr, vf);
-        if (j + 2 < n_tiles) load_tile<T>(kh, (j + 2) * T::BC, n, kbuf(j & 1), dma);
-        if (j + 1 < n_tiles) load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), dma);
-        if (!act) continue;  // wave-uniform: fully masked for this wave (causal)
-        if (act_next) {
+    char* kb[2];
+    char* vb[2];
+    kb[0] = k_lds0;
+    kb[1] = k_lds1;
+    vb[0] = v_lds0;
+    vb[1] = v_lds1;
+    general_tiles<T, CAUSAL, 2>(j, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma, fr, qf, s,
+                                oacc, scale_log2, m_run, l_run);
+    store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+}
+
+// ---- kernel, ping-pong schedule ---------------------------------------------------------------
+// Eight waves, two groups of four: the hardware deals the waves of a workgroup round-robin to
+// the four SIMDs of the CU, so waves w and w+4 share a SIMD. Every wave alternates two phases
+// per K/V tile, separated by workgroup barriers:
+//   softmax phase S_j: fragment reads of K_{j+1} and V_j from LDS (for the next phase),
+//                      interleaved with the softmax of tile j (P_j, row sums, rare exact
+//                      rescale of O) on the VALU;
+//   matrix phase  M_j: S_{j+1} = K_{j+1} Q^T and O += P_j V_j (sixteen MFMAs at D = 128) and
+//                      the wave's share of the K/V refill.
+// Group 1 runs one phase behind group 0 (group 0: S_j in global phase 2j, M_j in 2j+1), so in
+// every phase one wave of each SIMD feeds the matrix pipe while the other works on the VALU and
+// the LDS, and only four waves read LDS at a time, each a whole phase ahead of its use.
+// K_t and V_t live in buffer t % 3. In M_j group 0 requests K_{j+3} and V_{j+2}, group 1
+// requests K_{j+4} and V_{j+3} (its M_{-1} is an extra first phase); every request must land by
+// the barrier that ends the next-but-one odd phase, so each wave waits with vmcnt(2) (its two
+// newest requests stay in flight) at the end of its odd phases. Each tile is thus requested 3
+// or 4 phases before its first read, and replaces a tile whose last read was in an earlier
+// phase. Tiles that need masking, the last tile and causal diagonal tiles go through
+// general_tiles afterwards.
+#ifndef FA_PP_PRIO
+#define FA_PP_PRIO 1
+#endif
+
+// Scheduler pattern: N times {R DS reads, V VALU instructions} (sched_group_barrier masks
+// 0x100 DS read, 0x002 VALU | 0x400 transcendental).
+#ifndef FA_PP_READS_PER
+#define FA_PP_READS_PER 3
+#endif
+#ifndef FA_PP_VALU_PER
+#define FA_PP_VALU_PER 6
+#endif
+template <int R, int V, int N>
+__device__ __forceinline__ void sched_reads_valu() {
 #pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb) {
-                s2[nb] = f32x16{};
+    for (int i = 0; i < N; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, V, 0);
+    }
+}
+
+// End of a phase: the wave's LDS reads have completed (and, with WAIT_DMA, all but its two
+// newest DMA requests), then the workgroup barrier. The waits are s_waitcnt builtins rather
+// than asm so that the compiler's own wait tracking sees them (it then adds no waits of its own
+// for DMA that has already landed); the empty asm statements keep LDS accesses from moving
+// across. s_waitcnt immediates (gfx9 layout): vmcnt in bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8.
+constexpr short WAIT_VM2_LGKM0 = 0x0072;                  // vmcnt(2) lgkmcnt(0)
+constexpr short WAIT_LGKM0 = static_cast<short>(0xC07F);  // lgkmcnt(0)
+template <bool WAIT_DMA>
+__device__ __forceinline__ void end_phase() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(WAIT_DMA ? WAIT_VM2_LGKM0 : WAIT_LGKM0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Softmax of a mask-free tile against the running max m (see qk_softmax_optimistic): P in
+// fp16, and l += row sum unless some p overflowed fp16, in which case `overflow` is set
+// (wave-uniform) and the caller redoes the tile exactly. The row sum runs in two independent
+// v_dot2 chains.
+template <class T>
+__device__ __forceinline__ void softmax_optimistic(const f32x16 (&s)[T::NB], float scale_log2,
+                                                   float m_run, float& l_run, bool& overflow,
+                                                   f16x8 (&p)[T::NB][2]) {
+    float sum0 = 0.0F;
+    float sum1 = 0.0F;
 #pragma unroll
-                for (int kk = 0; kk < T::KK; ++kk) s2[nb] = mfma32(kf[nb][kk], qf[kk], s2[nb]);
-            }
+    for (int nb = 0; nb < T::NB; ++nb) {
+        float e[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[r] = exp2_fast(fmaf(s[nb][r], scale_log2, -m_run));
+        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
+        sum0 = sum8_f16(p[nb][0], sum0);
+        sum1 = sum8_f16(p[nb][1], sum1);
+    }
+    const float sum = sum0 + sum1;
+    overflow = wave_any(!(sum < INFINITY));
+    const float l_new = l_run + sum;
+    l_run = overflow ? l_run : l_new;
+}
+
+// Matrix phase: S^T_{j+1} = K_{j+1} Q^T (one chain of KK MFMAs per 32-key block) interleaved
+// with O^T += V_j^T P_j^T (2*DB MFMAs per block, DB independent chains). `mid` (the refill)
+// is issued after the first two pairs, when the matrix pipe already has work queued.
+template <class T, class Mid>
+__device__ __forceinline__ void matrix_phase(const f16x8 (&kf)[T::NB][T::KK],
+                                             const f16x8 (&qf)[T::KK],
+                                             const f16x8 (&vf)[T::NB][2][T::DB],
+                                             const f16x8 (&p)[T::NB][2], f32x16 (&s)[T::NB],
+                                             f32x16 (&oacc)[T::DB], Mid&& mid) {
+    constexpr int NQK = T::NB * T::KK;
+    constexpr int NPV = T::NB * 2 * T::DB;
+    constexpr int NI = NQK > NPV ? NQK : NPV;
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) s[nb] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        if (i < NQK) {
+            const int nb = i / T::KK;
+            const int kk = i % T::KK;
+            s[nb] = mfma32(kf[nb][kk], qf[kk], s[nb]);
         }
-        const int kt = j * T::BC;
-        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
-        f16x8 p[T::NB][2];
-        float alpha;
-        bool rescale;
-        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale_o<T>(oacc, alpha);
-        pv_frags<T>(vf, p, oacc);
-        if (act_next) {
-#pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
+        if (i < NPV) {
+            const int nb = i / (2 * T::DB);
+            const int h = (i / T::DB) % 2;
+            const int db = i % T::DB;
+            oacc[db] = mfma32(vf[nb][h][db], p[nb][h], oacc[db]);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the alternation
+        if (i == 1) {
+            mid();
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+}
+
+template <class T, bool CAUSAL>
+__global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ o, int n, int bh_count, int n_qblocks, float scale_log2, int negate_q) {
+    static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
+    static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
+    static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
+    // Separate LDS objects per buffer, as in flash_fwd_pipelined.
+    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds2[T::TILE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_uniform(threadIdx.x >> 6);
+    const int grp = wave >> 2;
+    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
+    const f16* kh = k + head;
+    const f16* vh = v + head;
+    const int q0 = w.qb * T::BR;
+    const int qw = q0 + wave * 32;
+    const int qrow = qw + (lane & 31);
+    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
+    // Steady tiles are the same for the whole workgroup (both groups must pass the same
+    // barriers): those wave 0, the one with the fewest, can take without a mask and with an
+    // active successor.
+    const int n_act0 = g::wave_active_tiles(n, q0, 32, T::BC, n_tiles, CAUSAL);
+    const int n_steady = max(0, min(g::wave_unmasked_tiles(n, q0, T::BC, n_act0, CAUSAL),
+                                    n_act0 - 1));
+
+    // Buffer b (compile-time in the steady loop, so the compiler can tell the objects apart).
+    auto kbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? k_lds0 : (B == 1 ? k_lds1 : k_lds2);
+    };
+    auto vbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? v_lds0 : (B == 1 ? v_lds1 : v_lds2);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+
+    const TileDma<T> dma(wave, lane);
+    // Prologue: K_0, K_1, K_2, V_0, V_1 (tiles past the end read as zeros and are never used).
+    load_tile<T>(kh, 0, n, kbuf(I0{}), dma);
+    load_tile<T>(vh, 0, n, vbuf(I0{}), dma);
+    load_tile<T>(kh, T::BC, n, kbuf(I1{}), dma);
+    load_tile<T>(kh, 2 * T::BC, n, kbuf(I2{}), dma);
+    load_tile<T>(vh, T::BC, n, vbuf(I1{}), dma);
+    f16x8 qf[T::KK];
+    load_q<T>(q + head, qrow, n, lane, negate_q, qf);
+    const Frag<T> fr(lane);
+
+    f32x16 oacc[T::DB];
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db) oacc[db] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0F;
+
+    wait_vmem();
+    __syncthreads();
+    // Q has landed on every path (the compiler then never waits for it inside the loop).
+#pragma unroll
+    for (int kk = 0; kk < T::KK; ++kk) asm volatile("" ::"v"(qf[kk]));
+    f32x16 s[T::NB];
+    if (n_act > 0) qk_tile<T>(kbuf(I0{}), fr, qf, s);
+
+    // The steady phases, compiled once per group so that every wait and refill of a wave is
+    // unconditional code (the compiler then tracks exactly which DMA has landed).
+    auto steady = [&](auto group) {
+        constexpr int G = decltype(group)::value;
+        // Requests of K_a into buffer a % 3 and V_b into buffer b % 3 (PA, PB: those buffers).
+        auto refill = [&](int a, auto pa, int b, auto pb) {
+            load_tile<T>(kh, a * T::BC, n, kbuf(pa), dma);
+            load_tile<T>(vh, b * T::BC, n, vbuf(pb), dma);
+        };
+        // The first phase ends only after every wave's QK_0 read of K buffer 0 (refilled below).
+        end_phase<false>();
+        if constexpr (G == 1) {  // group 1's M_{-1}: requests K_3 and V_2, then waits a phase
+            refill(3, I0{}, 2, I2{});
+            end_phase<false>();
+        }
+        auto tile = [&](int jj, auto r) {
+            constexpr int R = decltype(r)::value;  // jj % 3
+            using Rj = std::integral_constant<int, R>;
+            using Rj1 = std::integral_constant<int, (R + 1) % 3>;
+            using Rj2 = std::integral_constant<int, (R + 2) % 3>;
+            // softmax phase S_jj
+            f16x8 kf[T::NB][T::KK];
+            f16x8 vf[T::NB][2][T::DB];
+            load_k_frags<T>(kbuf(Rj1{}), fr, kf);
+            load_v_frags<T>(vbuf(Rj{}), fr, vf);
+            f16x8 p[T::NB][2];
+            bool overflow;
+            softmax_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
+            // A wave issues in order, so 24 fragment reads in a row would stall its softmax
+            // behind the LDS queue; spread them over the VALU work instead.
+            sched_reads_valu<FA_PP_READS_PER, FA_PP_VALU_PER,
+                             (T::NB * T::KK + T::NB * 4 * T::DB) / FA_PP_READS_PER>();
+            if (overflow) {  // rare: the exact softmax of this tile, new max, rescaled O
+                float alpha;
+                bool rescale;
+                softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+                if (rescale) rescale_o<T>(oacc, alpha);
+            }
+            end_phase<G == 1>();
+            // matrix phase M_jj
+            __builtin_amdgcn_s_setprio(FA_PP_PRIO);
+            matrix_phase<T>(kf, qf, vf, p, s, oacc, [&] {
+                if constexpr (G == 0) {
+                    refill(jj + 3, Rj{}, jj + 2, Rj2{});
+                } else {
+                    refill(jj + 4, Rj1{}, jj + 3, Rj{});
+                }
+            });
+            __builtin_amdgcn_s_setprio(0);
+            end_phase<G == 0>();
+        };
+        int jj = 0;
+        for (; jj + 3 <= n_steady; jj += 3) {
+            tile(jj, I0{});
+            tile(jj + 1, I1{});
+            tile(jj + 2, I2{});
+        }
+        if (jj < n_steady) tile(jj, I0{});
+        if (jj + 1 < n_steady) tile(jj + 1, I1{});
+        if constexpr (G == 0) end_phase<false>();  // group 0 waits out group 1's last matrix phase
+    };
+    if (n_steady > 0) {
+        if (grp == 0) {
+            steady(I0{});
+        } else {
+            steady(I1{});
+        }
+    }
+    char* kb[3];
+    char* vb[3];
+    kb[0] = k_lds0;
+    kb[1] = k_lds1;
+    kb[2] = k_lds2;
+    vb[0] = v_lds0;
+    vb[1] = v_lds1;
+    vb[2] = v_lds2;
+    general_tiles<T, CAUSAL, 3>(n_steady, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma,
+                                fr, qf, s, oacc, scale_log2, m_run, l_run);
     store_o<T>(o + head, qrow, n, lane, l_run, oacc);
 }
 
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
 // (csrc/kernels/flash_fwd.cu:597-612), chosen for MI355X by a sweep. Each entry is
-// "BC, NW, LAZY, PIPE" and can be overridden at build time with -DFA_<NAME>="bc, nw, lazy, pipe"
+// "BC, NW, LAZY, SCHED" and can be overridden at build time with -DFA_<NAME>="bc, nw, lazy, sched"
 // (the counterpart of bench/tune.sh, which rewrites those lines with sed).
 #ifndef FA_BASE_D64
-#define FA_BASE_D64 64, 4, false, false
+#define FA_BASE_D64 64, 4, false, SIMPLE
 #endif
 #ifndef FA_BASE_D128
-#define FA_BASE_D128 64, 4, false, false
+#define FA_BASE_D128 64, 4, false, SIMPLE
 #endif
 #ifndef FA_OPT_D64
-#define FA_OPT_D64 32, 4, true, true
+#define FA_OPT_D64 32, 4, true, PIPE
 #endif
 #ifndef FA_OPT_D64_CAUSAL
-#define FA_OPT_D64_CAUSAL 32, 4, true, true
+#define FA_OPT_D64_CAUSAL 32, 4, true, PIPE
 #endif
 #ifndef FA_OPT_D128
-#define FA_OPT_D128 32, 8, true, true
+#define FA_OPT_D128 32, 8, true, PINGPONG
 #endif
 #ifndef FA_OPT_D128_CAUSAL
-#define FA_OPT_D128_CAUSAL 32, 8, true, true
+#define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG
 #endif
 using BaseD64 = Tile<64, FA_BASE_D64>;
 using BaseD128 = Tile<128, FA_BASE_D128>;
@@ -752,7 +1001,9 @@ int launch(const fa_params& p, hipStream_t stream, float scale_log2, int negate_
     void* args[] = {&qp, &kp, &vp, &op, &n, &bh, &nqb, &scale_log2, &negate_q};
     const dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh));
     const void* fn;
-    if constexpr (T::PIPE) {
+    if constexpr (T::SCHED == PINGPONG) {
+        fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
+    } else if constexpr (T::SCHED == PIPE) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pipelined<T, CAUSAL>);
     } else {
         fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL>);

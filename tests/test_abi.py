@@ -105,7 +105,8 @@ def test_tile_config():
                 t = native.tile_config(d, causal, var)
                 assert t["block_q"] == 32 * t["waves"]
                 assert t["block_k"] % 32 == 0
-                assert t["lds_bytes"] == 4 * t["block_k"] * 2 * d
+                # two or three K/V tile buffers each, depending on the schedule
+                assert t["lds_bytes"] in (4 * t["block_k"] * 2 * d, 6 * t["block_k"] * 2 * d)
                 assert t["lds_bytes"] <= 160 * 1024
     assert native.tile_config(64, False, "fp16acc") == native.tile_config(64, False, "opt")
     with pytest.raises(ValueError, match="head_dim"):
