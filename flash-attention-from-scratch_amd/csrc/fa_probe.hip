@@ -1,0 +1,153 @@
+// Measurement probes for MI355X (gfx950): how fast can a CU stream fp16 MFMAs when the power
+// limit, not the schedule, sets the clock? Not part of the attention library; built into
+// fa/libfa_probe.so by fa_build.py (target "probe") and run by `python -m fa.probe`.
+//
+// probe_kernel<VALU, LDS>: 8 waves per workgroup (two per SIMD), one workgroup per CU slot,
+// each wave streaming v_mfma_f32_32x32x16_f16 on operands drawn from random fp16 data (the
+// data activity of attention, which sets the power draw). Per 16 MFMAs a wave optionally adds
+//   VALU: the VALU work of one softmax tile (16 v_exp_f32, 16 fma, adds), and
+//   LDS:  the fragment reads of one K/V tile (8 ds_read_b128 + 16 ds_read_b64_tr_b16, with the
+//         conflict-free access pattern of the attention kernel) feeding the MFMA operands.
+// Each workgroup records shader cycles (s_memtime) and 100 MHz real time (s_memrealtime), so
+// the effective clock is measured, not assumed.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "fa_device.h"
+
+namespace {
+
+using namespace fa::dev;
+
+template <int VALU, int LDS>
+__global__ __launch_bounds__(512) void probe_kernel(const f16x8* __restrict__ src, float* out,
+                                                    unsigned long long* clk, int iters) {
+    __shared__ __attribute__((aligned(1024))) char lds[32768];
+    const int t = threadIdx.x;
+    for (int i = t; i < 32768 / 16; i += 512) reinterpret_cast<f16x8*>(lds)[i] = src[i & 4095];
+    __syncthreads();
+    f16x8 a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = src[(t * 16 + i) & 4095];
+        b[i] = src[(t * 16 + 8 + i) & 4095];
+    }
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    float e[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) e[i] = (t & 63) * 1e-3F - i * 0.1F;
+    const int lane = t & 63;
+    // K-fragment and V^T-fragment offsets with the 64-bank swizzle of the attention kernel;
+    // every address stays inside the 32 KiB array.
+    const unsigned kbase = (lane & 31) * 256 + 16 * ((lane >> 5) ^ ((lane & 31) & 15));
+    const unsigned vbase = 16384 + ((lane & 15) >> 2) * 256 + 8 * (lane & 3) + 64 * (lane >> 4);
+    const unsigned long long s0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    float acc = 0.0F;
+    for (int it = 0; it < iters; ++it) {
+        if (LDS) {
+            f32x4 r[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                r[k] = *reinterpret_cast<const f32x4*>(lds + ((kbase + k * 32 + (it & 1) * 8192) & 16383));
+            f16x4 w[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) w[k] = lds_read_tr16(lds + ((vbase + k * 1024) & 32767));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                a[k] = __builtin_bit_cast(f16x8, r[k]);
+                b[k] = f16x8{w[2 * k][0], w[2 * k][1], w[2 * k][2], w[2 * k][3],
+                             w[2 * k + 1][0], w[2 * k + 1][1], w[2 * k + 1][2], w[2 * k + 1][3]};
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            c0 = mfma32(a[m], b[m], c0);
+            c1 = mfma32(a[m + 4], b[m + 1], c1);
+            c2 = mfma32(a[(m + 2) & 7], b[m + 2], c2);
+            c3 = mfma32(a[(m + 5) & 7], b[m + 3], c3);
+        }
+        if (VALU) {
+            float sum = 0.0F;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float x = exp2_fast(fmaf(c0[i], 0.125F, -e[i]));
+                e[i] = x * 0.5F;
+                sum += x;
+            }
+            acc += sum;
+        }
+        if (!LDS) asm volatile("" : "+v"(a[0]), "+v"(b[0]), "+v"(a[1]), "+v"(b[1]));
+    }
+    const unsigned long long s1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    out[blockIdx.x * 512 + t] = c0[0] + c1[1] + c2[2] + c3[3] + acc;
+    if (t == 0) {
+        clk[blockIdx.x * 2] = s1 - s0;
+        clk[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Runs the probe: `blocks` workgroups of 8 waves, `iters` iterations of 16 MFMAs per wave.
+// Returns the HIP status; *ms is the kernel time, *ghz the mean measured clock, *cycles the mean
+// shader cycles per workgroup.
+int fa_probe_ceiling(int valu, int lds, int blocks, int iters, float* ms, double* ghz,
+                     double* cycles) {
+    if (blocks <= 0 || blocks > 65536 || iters <= 0) return static_cast<int>(hipErrorInvalidValue);
+    f16x8* src = nullptr;
+    float* d = nullptr;
+    unsigned long long* c = nullptr;
+    hipError_t err = hipMalloc(&src, 4096 * sizeof(f16x8));
+    if (err == hipSuccess) err = hipMalloc(&d, static_cast<size_t>(blocks) * 512 * sizeof(float));
+    if (err == hipSuccess) err = hipMalloc(&c, static_cast<size_t>(blocks) * 2 * sizeof(unsigned long long));
+    if (err != hipSuccess) return static_cast<int>(err);
+    // Random fp16 in [-2, 2) from a 32-bit LCG.
+    static f16x8 host[4096];
+    uint32_t x = 12345U;
+    for (auto& h : host)
+        for (int j = 0; j < 8; ++j) {
+            x = x * 1103515245U + 12345U;
+            h[j] = static_cast<f16>(static_cast<float>((x >> 8) & 0xffffU) / 16384.0F - 2.0F);
+        }
+    (void)hipMemcpy(src, host, sizeof(host), hipMemcpyHostToDevice);
+    auto launch = [&](int it) {
+        if (valu && lds) hipLaunchKernelGGL((probe_kernel<1, 1>), dim3(blocks), dim3(512), 0, 0, src, d, c, it);
+        else if (valu) hipLaunchKernelGGL((probe_kernel<1, 0>), dim3(blocks), dim3(512), 0, 0, src, d, c, it);
+        else if (lds) hipLaunchKernelGGL((probe_kernel<0, 1>), dim3(blocks), dim3(512), 0, 0, src, d, c, it);
+        else hipLaunchKernelGGL((probe_kernel<0, 0>), dim3(blocks), dim3(512), 0, 0, src, d, c, it);
+    };
+    hipEvent_t e0, e1;
+    (void)hipEventCreate(&e0);
+    (void)hipEventCreate(&e1);
+    launch(200);
+    launch(iters);  // ramp the clock before the timed launch
+    (void)hipEventRecord(e0, nullptr);
+    launch(iters);
+    (void)hipEventRecord(e1, nullptr);
+    err = hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(ms, e0, e1);
+    unsigned long long* hc = new unsigned long long[2 * static_cast<size_t>(blocks)];
+    (void)hipMemcpy(hc, c, static_cast<size_t>(blocks) * 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    double sg = 0.0;
+    double sc = 0.0;
+    for (int i = 0; i < blocks; ++i) {
+        sg += static_cast<double>(hc[2 * i]) / (static_cast<double>(hc[2 * i + 1]) * 10.0);
+        sc += static_cast<double>(hc[2 * i]);
+    }
+    *ghz = sg / blocks;
+    *cycles = sc / blocks;
+    delete[] hc;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipFree(src);
+    (void)hipFree(d);
+    (void)hipFree(c);
+    return err == hipSuccess ? static_cast<int>(hipGetLastError()) : static_cast<int>(err);
+}
+
+}  // extern "C"

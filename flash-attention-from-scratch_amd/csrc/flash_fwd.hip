@@ -40,6 +40,31 @@
 #include "fa_geometry.h"
 #include "fa_hip.h"
 
+// Clock probe (only in the fa/libfa_hip_clock.so build, -DFA_CLOCK_PROBE=1): each workgroup of
+// the main kernels records its shader cycles and its 100 MHz real time, from which the clock the
+// kernel actually ran at follows. Compiled out of the library proper.
+#ifndef FA_CLOCK_PROBE
+#define FA_CLOCK_PROBE 0
+#endif
+#if FA_CLOCK_PROBE
+__device__ unsigned long long g_fa_clock[65536][2];
+#define FA_CLOCK_BEGIN()                                                  \
+    const unsigned long long fa_c0 = __builtin_amdgcn_s_memtime();        \
+    const unsigned long long fa_r0 = __builtin_amdgcn_s_memrealtime()
+#define FA_CLOCK_END()                                                    \
+    do {                                                                  \
+        const unsigned long long fa_c1 = __builtin_amdgcn_s_memtime();    \
+        const unsigned long long fa_r1 = __builtin_amdgcn_s_memrealtime(); \
+        if (threadIdx.x == 0 && blockIdx.x < 65536) {                     \
+            g_fa_clock[blockIdx.x][0] = fa_c1 - fa_c0;                    \
+            g_fa_clock[blockIdx.x][1] = fa_r1 - fa_r0;                    \
+        }                                                                 \
+    } while (0)
+#else
+#define FA_CLOCK_BEGIN() static_cast<void>(0)
+#define FA_CLOCK_END() static_cast<void>(0)
+#endif
+
 namespace fa {
 namespace {
 
@@ -561,6 +586,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
+    FA_CLOCK_BEGIN();
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -663,6 +689,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     general_tiles<T, CAUSAL, 2>(j, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma, fr, qf, s,
                                 oacc, scale_log2, m_run, l_run);
     store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+    FA_CLOCK_END();
 }
 
 // ---- kernel, ping-pong schedule ---------------------------------------------------------------
@@ -789,6 +816,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
+    FA_CLOCK_BEGIN();
     // Separate LDS objects per buffer, as in flash_fwd_pipelined.
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
@@ -886,14 +914,17 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
             // behind the LDS queue; spread them over the VALU work instead.
             sched_reads_valu<FA_PP_READS_PER, FA_PP_VALU_PER,
                              (T::NB * T::KK + T::NB * 4 * T::DB) / FA_PP_READS_PER>();
-            if (overflow) {  // rare: the exact softmax of this tile, new max, rescaled O
-                float alpha;
+            // No branch here: the phase ends as soon as the softmax is issued, without waiting
+            // for its results. The overflow test is taken at the start of the matrix phase,
+            // before S is overwritten, when its flag has long been computed.
+            end_phase<G == 1>();
+            // matrix phase M_jj
+            if (__builtin_expect(overflow, 0)) {  // rare: exact softmax of this tile, new max,
+                float alpha;                       // rescaled O
                 bool rescale;
                 softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
                 if (rescale) rescale_o<T>(oacc, alpha);
             }
-            end_phase<G == 1>();
-            // matrix phase M_jj
             __builtin_amdgcn_s_setprio(FA_PP_PRIO);
             matrix_phase<T>(kf, qf, vf, p, s, oacc, [&] {
                 if constexpr (G == 0) {
@@ -933,6 +964,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     general_tiles<T, CAUSAL, 3>(n_steady, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma,
                                 fr, qf, s, oacc, scale_log2, m_run, l_run);
     store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+    FA_CLOCK_END();
 }
 
 // ---- tile table -------------------------------------------------------------------------------
@@ -1051,6 +1083,14 @@ bool tile_of(int head_dim, bool causal, int variant, fa_tile_info* out) {
 }  // namespace fa
 
 extern "C" {
+
+#if FA_CLOCK_PROBE
+// Copies the per-workgroup (shader cycles, 10 ns ticks) pairs of the last launch into `host`
+// (65536 x 2 entries). Exists only in the clock-probe build.
+int fa_probe_clock_fetch(unsigned long long* host) {
+    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fa_clock), sizeof(g_fa_clock)));
+}
+#endif
 
 const char* fa_last_error(void) { return fa::g_last_error.c_str(); }
 

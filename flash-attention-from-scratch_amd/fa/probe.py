@@ -1,0 +1,140 @@
+"""Power and clock measurements on MI355X (not part of the attention API).
+
+    PYTHONPATH=flash-attention-from-scratch_amd python3 -m fa.probe [ceiling] [clock] [busy]
+
+ceiling: TFLOPS and measured clock of pure v_mfma_f32_32x32x16_f16 streams on random fp16
+         operands (8 waves per CU), alone and with the per-tile VALU work and LDS fragment reads
+         of attention added (fa/libfa_probe.so, csrc/fa_probe.hip).
+clock:   the clock the attention kernels themselves run at, and their shader cycles per
+         workgroup, on the benchmark shapes (fa/libfa_hip_clock.so: the library built with
+         per-workgroup s_memtime / s_memrealtime recording).
+busy:    the same for cfg4's non-causal kernel with 16, 8, 4, 2 and 1 heads: with fewer busy CUs
+         the clock rises at unchanged cycles per workgroup when chip power is the limit.
+Prints one JSON line per measurement. Build first: fa_build.py --only probe.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import math
+import statistics
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PEAK_TFLOPS = 2516.6
+
+
+def _emit(rec: dict) -> None:
+    print(json.dumps(rec), flush=True)
+
+
+def ceiling(blocks: int = 1024, iters: int = 2000) -> None:
+    so = ctypes.CDLL(str(HERE / "libfa_probe.so"))
+    so.fa_probe_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.POINTER(ctypes.c_float),
+                                    ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_double)]
+    for valu, lds in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        ms, ghz, cyc = ctypes.c_float(), ctypes.c_double(), ctypes.c_double()
+        rc = so.fa_probe_ceiling(valu, lds, blocks, iters, ctypes.byref(ms), ctypes.byref(ghz),
+                                 ctypes.byref(cyc))
+        if rc != 0:
+            raise RuntimeError(f"fa_probe_ceiling failed with HIP status {rc}")
+        flops = blocks * 8 * iters * 16 * 32768.0
+        tf = flops / (ms.value * 1e-3) / 1e12
+        _emit({"probe": "mfma_ceiling", "softmax_valu": bool(valu), "lds_fragments": bool(lds),
+               "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
+               "clock_ghz": round(ghz.value, 3),
+               "cycles_per_16_mfma_per_simd": round(cyc.value / iters, 1)})
+
+
+def _clock_lib():
+    from fa import native
+
+    so = ctypes.CDLL(str(HERE / "libfa_hip_clock.so"))
+    so.fa_flash_fwd.argtypes = [ctypes.POINTER(native.FaParams), ctypes.c_void_p]
+    so.fa_flash_fwd.restype = ctypes.c_int
+    so.fa_last_error.restype = ctypes.c_char_p
+    so.fa_probe_clock_fetch.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    return so
+
+
+def _run_clock(so, q, k, v, causal: bool, reps: int = 20):
+    import numpy as np
+    import torch
+
+    from fa import native
+
+    b, h, n, d = q.shape
+    o = torch.empty_like(q)
+    p = native.make_params(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, n, d,
+                           1.0 / math.sqrt(d), causal, "opt")
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(reps):
+        rc = so.fa_flash_fwd(ctypes.byref(p), ctypes.c_void_p(stream))
+        if rc != 0:
+            raise RuntimeError(so.fa_last_error().decode())
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        so.fa_flash_fwd(ctypes.byref(p), ctypes.c_void_p(stream))
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    buf = (ctypes.c_ulonglong * (65536 * 2))()
+    so.fa_probe_clock_fetch(buf)
+    tile = native.tile_config(d, causal, "opt")
+    n_wg = b * h * ((n + tile["block_q"] - 1) // tile["block_q"])
+    arr = np.frombuffer(buf, dtype=np.uint64).reshape(65536, 2)[:n_wg].astype(np.float64)
+    ghz = arr[:, 0] / (arr[:, 1] * 10.0)
+    return statistics.median(times), float(np.median(ghz)), float(np.median(arr[:, 0])), n_wg
+
+
+def clock() -> None:
+    import torch
+
+    from fa.configs import CONFIGS, make_inputs
+
+    so = _clock_lib()
+    for name in ("cfg4", "cfg2", "cfg5"):
+        cfg = CONFIGS[name]
+        q, k, v = make_inputs(cfg)
+        for causal in cfg.causal:
+            ms, ghz, cyc, n_wg = _run_clock(so, q, k, v, causal)
+            tf = cfg.flops(causal) / (ms * 1e-3) / 1e12
+            _emit({"probe": "kernel_clock", "config": name, "causal": causal, "workgroups": n_wg,
+                   "median_ms": round(ms, 4), "tflops": round(tf, 1),
+                   "clock_ghz_median": round(ghz, 3),
+                   "cycles_per_workgroup_median": round(cyc)})
+        del q, k, v
+        torch.cuda.empty_cache()
+
+
+def busy() -> None:
+    import torch
+
+    so = _clock_lib()
+    n, d = 16384, 128
+    for heads in (16, 8, 4, 2, 1):
+        g = torch.Generator().manual_seed(0)
+        q, k, v = (torch.randn(1, heads, n, d, generator=g).half().cuda() for _ in range(3))
+        ms, ghz, cyc, n_wg = _run_clock(so, q, k, v, False, reps=10)
+        tf = 4.0 * heads * n * n * d / (ms * 1e-3) / 1e12
+        _emit({"probe": "busy_cus", "heads": heads, "workgroups": n_wg, "median_ms": round(ms, 4),
+               "tflops": round(tf, 1), "clock_ghz_median": round(ghz, 3),
+               "cycles_per_workgroup_median": round(cyc)})
+
+
+def main(argv: list[str]) -> int:
+    what = argv or ["ceiling", "clock", "busy"]
+    for w in what:
+        {"ceiling": ceiling, "clock": clock, "busy": busy}[w]()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))

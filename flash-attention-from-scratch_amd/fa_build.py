@@ -9,6 +9,8 @@ Targets (outputs are git-ignored; they travel to the GPU box with the source tre
   blocks  tests/blocks/libfa_blocks.so   building-block kernels for the GPU unit tests
   oracle  oracle/liboracle_fp64.so       the C fp64 oracle (gcc), test infrastructure only
   geom    tests/geometry/libfa_geom.so   host build of the tile geometry, for the CPU tests
+  probe   fa/libfa_probe.so, fa/libfa_hip_clock.so   measurement only (python -m fa.probe):
+          MFMA power-ceiling probes, and the kernels with per-workgroup clock recording
 
 Counterpart of the reference's setup.py / CMakeLists.txt / Makefile build targets
 (setup.py:12-33, CMakeLists.txt:56-87, Makefile:21-32): the kernel library is compiled by
@@ -127,9 +129,18 @@ def build_geom() -> Path:
     return out
 
 
+def build_probe() -> list[Path]:
+    out = FA / "libfa_probe.so"
+    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{CSRC}", str(CSRC / "fa_probe.hip"), "-o", str(out)])
+    clock = FA / "libfa_hip_clock.so"
+    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", "-DFA_CLOCK_PROBE=1",
+          str(CSRC / "flash_fwd.hip"), "-o", str(clock)])
+    return [out, clock]
+
+
 TARGETS = {"lib": build_lib, "ext": build_ext, "blocks": build_blocks, "oracle": build_oracle,
-           "geom": build_geom}
-ALL = ("lib", "ext", "blocks", "oracle", "geom")
+           "geom": build_geom, "probe": build_probe}
+ALL = ("lib", "ext", "blocks", "oracle", "geom", "probe")
 
 
 def build_all() -> None:
