@@ -997,6 +997,24 @@ using OptD64Causal = Tile<64, FA_OPT_D64_CAUSAL>;
 using OptD128 = Tile<128, FA_OPT_D128>;
 using OptD128Causal = Tile<128, FA_OPT_D128_CAUSAL>;
 
+// Runtime choice by sequence length (the reference fixes one tile per (variant, d, causal)):
+// in causal attention over a short sequence most tiles of a 256-row workgroup lie on the
+// diagonal band, which the ping-pong kernel runs through its masked path; there a 128-row
+// workgroup with the simple schedule is faster. Crossover measured between N = 2048 and 4096
+// (FA2-paper shapes, B*N = 16k tokens).
+#ifndef FA_SHORT_CAUSAL_MAX_N
+#define FA_SHORT_CAUSAL_MAX_N 2048
+#endif
+#ifndef FA_OPT_D128_CAUSAL_SHORT
+#define FA_OPT_D128_CAUSAL_SHORT 64, 4, true, SIMPLE
+#endif
+using OptD128CausalShort = Tile<128, FA_OPT_D128_CAUSAL_SHORT>;
+
+bool short_causal(int head_dim, bool causal, int variant, int seqlen) {
+    return causal && head_dim == 128 && variant != FA_VARIANT_BASELINE &&
+           seqlen <= FA_SHORT_CAUSAL_MAX_N;
+}
+
 // One tile per (head dim, causal) for a variant (the reference's KernelSet,
 // csrc/kernels/flash_fwd.cu:582-591).
 template <class D64, class D64C, class D128, class D128C>
@@ -1072,10 +1090,14 @@ fa_tile_info info_for(int head_dim, bool causal) {
                   : info_of<typename Set::template Pick<false, 128>>();
 }
 
-bool tile_of(int head_dim, bool causal, int variant, fa_tile_info* out) {
+bool tile_of(int head_dim, bool causal, int variant, int seqlen, fa_tile_info* out) {
     if (head_dim != 64 && head_dim != 128) return false;
-    *out = variant == FA_VARIANT_BASELINE ? info_for<BaseSet>(head_dim, causal)
-                                          : info_for<OptSet>(head_dim, causal);
+    if (short_causal(head_dim, causal, variant, seqlen)) {
+        *out = info_of<OptD128CausalShort>();
+    } else {
+        *out = variant == FA_VARIANT_BASELINE ? info_for<BaseSet>(head_dim, causal)
+                                              : info_for<OptSet>(head_dim, causal);
+    }
     return true;
 }
 
@@ -1096,13 +1118,15 @@ const char* fa_last_error(void) { return fa::g_last_error.c_str(); }
 
 const char* fa_version(void) { return "fa_hip 0.1.0 gfx950"; }
 
-int fa_tile_config(int32_t head_dim, int32_t causal, int32_t variant, fa_tile_info* out) {
+int fa_tile_config(int32_t head_dim, int32_t causal, int32_t variant, int32_t seqlen,
+                   fa_tile_info* out) {
     fa::g_last_error.clear();
     if (out == nullptr) return fa::fail(FA_EINVAL, "fa_tile_config: out must not be NULL");
     if (variant < FA_VARIANT_BASELINE || variant > FA_VARIANT_FP16ACC) {
         return fa::fail(FA_EINVAL, "fa_tile_config: unknown variant");
     }
-    if (!fa::tile_of(head_dim, causal != 0, variant, out)) {
+    if (seqlen <= 0) return fa::fail(FA_EINVAL, "fa_tile_config: seqlen must be positive");
+    if (!fa::tile_of(head_dim, causal != 0, variant, seqlen, out)) {
         return fa::fail(FA_EINVAL, "fa_tile_config: head_dim must be 64 or 128, got " +
                                        std::to_string(head_dim));
     }
@@ -1143,7 +1167,7 @@ int fa_flash_fwd(const fa_params* params, void* stream) {
         return fail(FA_EINVAL, "flash_fwd: seqlen * head_dim must be below 2^31");
     }
     fa_tile_info t{};
-    fa::tile_of(p.head_dim, p.causal != 0, p.variant, &t);
+    fa::tile_of(p.head_dim, p.causal != 0, p.variant, p.seqlen, &t);
     const int64_t blocks = static_cast<int64_t>(p.batch) * p.heads *
                            ((static_cast<int64_t>(p.seqlen) + t.block_q - 1) / t.block_q);
     if (blocks > INT32_MAX) {
@@ -1164,6 +1188,9 @@ int fa_flash_fwd(const fa_params* params, void* stream) {
     if (scale_log2 < 1.17549435e-38F) scale_log2 = 1.17549435e-38F;
 
     auto s = static_cast<hipStream_t>(stream);
+    if (fa::short_causal(p.head_dim, p.causal != 0, p.variant, p.seqlen)) {
+        return fa::launch<fa::OptD128CausalShort, true>(p, s, scale_log2, negate_q);
+    }
     if (p.variant == FA_VARIANT_BASELINE) {
         return fa::dispatch<fa::BaseSet>(p, s, scale_log2, negate_q);
     }

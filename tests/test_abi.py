@@ -102,13 +102,20 @@ def test_tile_config():
     for d in (64, 128):
         for causal in (False, True):
             for var in ("baseline", "opt", "fp16acc"):
-                t = native.tile_config(d, causal, var)
+              for n in (1, 2048, 2049, 16384):
+                t = native.tile_config(d, causal, var, n)
                 assert t["block_q"] == 32 * t["waves"]
                 assert t["block_k"] % 32 == 0
                 # two or three K/V tile buffers each, depending on the schedule
                 assert t["lds_bytes"] in (4 * t["block_k"] * 2 * d, 6 * t["block_k"] * 2 * d)
                 assert t["lds_bytes"] <= 160 * 1024
     assert native.tile_config(64, False, "fp16acc") == native.tile_config(64, False, "opt")
+    # causal d=128: short sequences get 128-row workgroups, long ones the 256-row ping-pong tile
+    assert native.tile_config(128, True, "opt", 2048)["block_q"] == 128
+    assert native.tile_config(128, True, "opt", 2049)["block_q"] == 256
+    assert native.tile_config(128, False, "opt", 512)["block_q"] == 256
+    with pytest.raises(ValueError, match="seqlen"):
+        native.tile_config(128, True, "opt", 0)
     with pytest.raises(ValueError, match="head_dim"):
         native.tile_config(96, False)
     with pytest.raises(ValueError, match="variant"):
