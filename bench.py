@@ -204,9 +204,8 @@ def main() -> int:
                 "algorithmic_bytes": cfg.bytes(),
                 "launch_ms": pm["avg_launch_ms"]}
 
-    tile = {("causal" if c else "non_causal"): native.tile_config(cfg.head_dim, c, args.variant,
-                                                                  cfg.seqlen)
-            for c in modes}
+    tile = {("causal" if c else "non_causal"): native.tile_config(
+        cfg.head_dim, c, args.variant, cfg.seqlen, cfg.batch, cfg.heads) for c in modes}
     result = {
         "metric": "attention fwd TFLOPS (4BHN^2d, /2 causal) and % of MI355X fp16 MFMA peak",
         "value": round(value, 2),

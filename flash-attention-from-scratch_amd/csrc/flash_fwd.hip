@@ -969,62 +969,139 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
-// (csrc/kernels/flash_fwd.cu:597-612), chosen for MI355X by a sweep. Each entry is
-// "BC, NW, LAZY, SCHED" and can be overridden at build time with -DFA_<NAME>="bc, nw, lazy, sched"
-// (the counterpart of bench/tune.sh, which rewrites those lines with sed).
+// (csrc/kernels/flash_fwd.cu:597-612). On MI355X the best tile also depends on the sequence
+// length, so the "opt" / "fp16acc" rows are split by N at thresholds found by the tile sweep
+// (FA2-paper shapes, B*N = 16k tokens): short sequences favour 256-row workgroups with the
+// simple schedule (less pipeline prologue and epilogue per workgroup, fewer diagonal tiles
+// on the ping-pong's masked path), long ones the ping-pong or pipelined schedules. Small grids
+// (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000) take 4-wave tiles, so
+// that each wave gets a SIMD of its own on twice as many CUs. Each entry is
+// "BC, NW, LAZY, SCHED" and can be overridden at build time with -DFA_<NAME>="..." (the
+// counterpart of bench/tune.sh, which rewrites the `using` lines with sed); so can each
+// threshold (a row applies while N <= its FA_*_MAX_N).
 #ifndef FA_BASE_D64
 #define FA_BASE_D64 64, 4, false, SIMPLE
 #endif
 #ifndef FA_BASE_D128
 #define FA_BASE_D128 64, 4, false, SIMPLE
 #endif
+#ifndef FA_OPT_D64_SMALL
+#define FA_OPT_D64_SMALL 64, 4, true, PIPE
+#endif
+#ifndef FA_OPT_D128_SMALL
+#define FA_OPT_D128_SMALL 64, 4, true, SIMPLE
+#endif
+#ifndef FA_OPT_D64_SHORT
+#define FA_OPT_D64_SHORT 64, 8, true, SIMPLE
+#endif
 #ifndef FA_OPT_D64
-#define FA_OPT_D64 32, 4, true, PIPE
+#define FA_OPT_D64 64, 8, true, PINGPONG
+#endif
+#ifndef FA_OPT_D64_CAUSAL_SHORT
+#define FA_OPT_D64_CAUSAL_SHORT 64, 8, true, SIMPLE
 #endif
 #ifndef FA_OPT_D64_CAUSAL
 #define FA_OPT_D64_CAUSAL 32, 4, true, PIPE
 #endif
+#ifndef FA_OPT_D64_CAUSAL_LONG
+#define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG
+#endif
 #ifndef FA_OPT_D128
 #define FA_OPT_D128 32, 8, true, PINGPONG
+#endif
+#ifndef FA_OPT_D128_CAUSAL_SHORT
+#define FA_OPT_D128_CAUSAL_SHORT 32, 4, true, SIMPLE
 #endif
 #ifndef FA_OPT_D128_CAUSAL
 #define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG
 #endif
-using BaseD64 = Tile<64, FA_BASE_D64>;
-using BaseD128 = Tile<128, FA_BASE_D128>;
-using OptD64 = Tile<64, FA_OPT_D64>;
-using OptD64Causal = Tile<64, FA_OPT_D64_CAUSAL>;
-using OptD128 = Tile<128, FA_OPT_D128>;
-using OptD128Causal = Tile<128, FA_OPT_D128_CAUSAL>;
-
-// Runtime choice by sequence length (the reference fixes one tile per (variant, d, causal)):
-// in causal attention over a short sequence most tiles of a 256-row workgroup lie on the
-// diagonal band, which the ping-pong kernel runs through its masked path; there a 128-row
-// workgroup with the simple schedule is faster. Crossover measured between N = 2048 and 4096
-// (FA2-paper shapes, B*N = 16k tokens).
-#ifndef FA_SHORT_CAUSAL_MAX_N
-#define FA_SHORT_CAUSAL_MAX_N 2048
+#ifndef FA_D64_SHORT_MAX_N
+#define FA_D64_SHORT_MAX_N 2048
 #endif
-#ifndef FA_OPT_D128_CAUSAL_SHORT
-#define FA_OPT_D128_CAUSAL_SHORT 64, 4, true, SIMPLE
+#ifndef FA_D64_CAUSAL_SHORT_MAX_N
+#define FA_D64_CAUSAL_SHORT_MAX_N 4096
 #endif
-using OptD128CausalShort = Tile<128, FA_OPT_D128_CAUSAL_SHORT>;
+#ifndef FA_D64_CAUSAL_MAX_N
+#define FA_D64_CAUSAL_MAX_N 8192
+#endif
+#ifndef FA_D128_CAUSAL_SHORT_MAX_N
+#define FA_D128_CAUSAL_SHORT_MAX_N 3072
+#endif
+#ifndef FA_SMALL_GRID_WGS
+#define FA_SMALL_GRID_WGS 256
+#endif
 
-bool short_causal(int head_dim, bool causal, int variant, int seqlen) {
-    return causal && head_dim == 128 && variant != FA_VARIANT_BASELINE &&
-           seqlen <= FA_SHORT_CAUSAL_MAX_N;
+// One kernel instance per row: the tile and whether it is the causal build.
+template <class T_, bool CAUSAL_>
+struct Entry {
+    using T = T_;
+    static constexpr bool CAUSAL = CAUSAL_;
+};
+enum TileId : int {
+    BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
+    OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
+    OPT_D64_SHORT, OPT_D64, OPT_D64_C_SHORT, OPT_D64_C, OPT_D64_C_LONG,
+    OPT_D128, OPT_D128_C_SHORT, OPT_D128_C,
+};
+template <int ID> struct Row;
+template <> struct Row<BASE_D64> : Entry<Tile<64, FA_BASE_D64>, false> {};
+template <> struct Row<BASE_D64_C> : Entry<Tile<64, FA_BASE_D64>, true> {};
+template <> struct Row<BASE_D128> : Entry<Tile<128, FA_BASE_D128>, false> {};
+template <> struct Row<BASE_D128_C> : Entry<Tile<128, FA_BASE_D128>, true> {};
+template <> struct Row<OPT_D64_SMALL> : Entry<Tile<64, FA_OPT_D64_SMALL>, false> {};
+template <> struct Row<OPT_D64_C_SMALL> : Entry<Tile<64, FA_OPT_D64_SMALL>, true> {};
+template <> struct Row<OPT_D128_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, false> {};
+template <> struct Row<OPT_D128_C_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, true> {};
+template <> struct Row<OPT_D64_SHORT> : Entry<Tile<64, FA_OPT_D64_SHORT>, false> {};
+template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
+template <> struct Row<OPT_D64_C_SHORT> : Entry<Tile<64, FA_OPT_D64_CAUSAL_SHORT>, true> {};
+template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
+template <> struct Row<OPT_D64_C_LONG> : Entry<Tile<64, FA_OPT_D64_CAUSAL_LONG>, true> {};
+template <> struct Row<OPT_D128> : Entry<Tile<128, FA_OPT_D128>, false> {};
+template <> struct Row<OPT_D128_C_SHORT> : Entry<Tile<128, FA_OPT_D128_CAUSAL_SHORT>, true> {};
+template <> struct Row<OPT_D128_C> : Entry<Tile<128, FA_OPT_D128_CAUSAL>, true> {};
+
+// The row for (head_dim in {64, 128}, causal, variant, seqlen >= 1, batch * heads >= 1).
+TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
+    if (variant == FA_VARIANT_BASELINE) {
+        if (head_dim == 64) return causal ? BASE_D64_C : BASE_D64;
+        return causal ? BASE_D128_C : BASE_D128;
+    }
+    if (bh * ((static_cast<int64_t>(n) + 255) / 256) < FA_SMALL_GRID_WGS) {
+        if (head_dim == 64) return causal ? OPT_D64_C_SMALL : OPT_D64_SMALL;
+        return causal ? OPT_D128_C_SMALL : OPT_D128_SMALL;
+    }
+    if (head_dim == 64) {
+        if (!causal) return n <= FA_D64_SHORT_MAX_N ? OPT_D64_SHORT : OPT_D64;
+        if (n <= FA_D64_CAUSAL_SHORT_MAX_N) return OPT_D64_C_SHORT;
+        return n <= FA_D64_CAUSAL_MAX_N ? OPT_D64_C : OPT_D64_C_LONG;
+    }
+    if (!causal) return OPT_D128;
+    return n <= FA_D128_CAUSAL_SHORT_MAX_N ? OPT_D128_C_SHORT : OPT_D128_C;
 }
 
-// One tile per (head dim, causal) for a variant (the reference's KernelSet,
-// csrc/kernels/flash_fwd.cu:582-591).
-template <class D64, class D64C, class D128, class D128C>
-struct KernelSet {
-    template <bool CAUSAL, int D>
-    using Pick = std::conditional_t<
-        D == 64, std::conditional_t<CAUSAL, D64C, D64>, std::conditional_t<CAUSAL, D128C, D128>>;
-};
-using BaseSet = KernelSet<BaseD64, BaseD64, BaseD128, BaseD128>;
-using OptSet = KernelSet<OptD64, OptD64Causal, OptD128, OptD128Causal>;
+// Calls f(Row<id>{}) with the row as a compile-time type.
+template <class F>
+decltype(auto) with_row(TileId id, F&& f) {
+    switch (id) {
+        case BASE_D64: return f(Row<BASE_D64>{});
+        case BASE_D64_C: return f(Row<BASE_D64_C>{});
+        case BASE_D128: return f(Row<BASE_D128>{});
+        case BASE_D128_C: return f(Row<BASE_D128_C>{});
+        case OPT_D64_SMALL: return f(Row<OPT_D64_SMALL>{});
+        case OPT_D64_C_SMALL: return f(Row<OPT_D64_C_SMALL>{});
+        case OPT_D128_SMALL: return f(Row<OPT_D128_SMALL>{});
+        case OPT_D128_C_SMALL: return f(Row<OPT_D128_C_SMALL>{});
+        case OPT_D64_SHORT: return f(Row<OPT_D64_SHORT>{});
+        case OPT_D64: return f(Row<OPT_D64>{});
+        case OPT_D64_C_SHORT: return f(Row<OPT_D64_C_SHORT>{});
+        case OPT_D64_C: return f(Row<OPT_D64_C>{});
+        case OPT_D64_C_LONG: return f(Row<OPT_D64_C_LONG>{});
+        case OPT_D128: return f(Row<OPT_D128>{});
+        case OPT_D128_C_SHORT: return f(Row<OPT_D128_C_SHORT>{});
+        default: return f(Row<OPT_D128_C>{});
+    }
+}
 
 template <class T>
 constexpr fa_tile_info info_of() {
@@ -1065,39 +1142,12 @@ int launch(const fa_params& p, hipStream_t stream, float scale_log2, int negate_
     return FA_OK;
 }
 
-template <class Set, int D>
-int dispatch_d(const fa_params& p, hipStream_t s, float scale_log2, int negate_q) {
-    return p.causal
-               ? launch<typename Set::template Pick<true, D>, true>(p, s, scale_log2, negate_q)
-               : launch<typename Set::template Pick<false, D>, false>(p, s, scale_log2, negate_q);
-}
-
-template <class Set>
-int dispatch(const fa_params& p, hipStream_t s, float scale_log2, int negate_q) {
-    return p.head_dim == 64 ? dispatch_d<Set, 64>(p, s, scale_log2, negate_q)
-                            : dispatch_d<Set, 128>(p, s, scale_log2, negate_q);
-}
-
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
 
-template <class Set>
-fa_tile_info info_for(int head_dim, bool causal) {
-    if (head_dim == 64) {
-        return causal ? info_of<typename Set::template Pick<true, 64>>()
-                      : info_of<typename Set::template Pick<false, 64>>();
-    }
-    return causal ? info_of<typename Set::template Pick<true, 128>>()
-                  : info_of<typename Set::template Pick<false, 128>>();
-}
-
-bool tile_of(int head_dim, bool causal, int variant, int seqlen, fa_tile_info* out) {
+bool tile_of(int head_dim, bool causal, int variant, int seqlen, int64_t bh, fa_tile_info* out) {
     if (head_dim != 64 && head_dim != 128) return false;
-    if (short_causal(head_dim, causal, variant, seqlen)) {
-        *out = info_of<OptD128CausalShort>();
-    } else {
-        *out = variant == FA_VARIANT_BASELINE ? info_for<BaseSet>(head_dim, causal)
-                                              : info_for<OptSet>(head_dim, causal);
-    }
+    *out = with_row(tile_id(head_dim, causal, variant, seqlen, bh),
+                    [](auto row) { return info_of<typename decltype(row)::T>(); });
     return true;
 }
 
@@ -1118,17 +1168,20 @@ const char* fa_last_error(void) { return fa::g_last_error.c_str(); }
 
 const char* fa_version(void) { return "fa_hip 0.1.0 gfx950"; }
 
-int fa_tile_config(int32_t head_dim, int32_t causal, int32_t variant, int32_t seqlen,
-                   fa_tile_info* out) {
+int fa_tile_config(const fa_params* params, fa_tile_info* out) {
     fa::g_last_error.clear();
-    if (out == nullptr) return fa::fail(FA_EINVAL, "fa_tile_config: out must not be NULL");
-    if (variant < FA_VARIANT_BASELINE || variant > FA_VARIANT_FP16ACC) {
-        return fa::fail(FA_EINVAL, "fa_tile_config: unknown variant");
+    if (params == nullptr || out == nullptr) {
+        return fa::fail(FA_EINVAL, "fa_tile_config: params and out must not be NULL");
     }
-    if (seqlen <= 0) return fa::fail(FA_EINVAL, "fa_tile_config: seqlen must be positive");
-    if (!fa::tile_of(head_dim, causal != 0, variant, seqlen, out)) {
+    const fa_params& p = *params;
+    if (p.variant > FA_VARIANT_FP16ACC) return fa::fail(FA_EINVAL, "fa_tile_config: unknown variant");
+    if (p.batch <= 0 || p.heads <= 0 || p.seqlen <= 0) {
+        return fa::fail(FA_EINVAL, "fa_tile_config: batch, heads and seqlen must be positive");
+    }
+    const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
+    if (!fa::tile_of(p.head_dim, p.causal != 0, p.variant, p.seqlen, bh, out)) {
         return fa::fail(FA_EINVAL, "fa_tile_config: head_dim must be 64 or 128, got " +
-                                       std::to_string(head_dim));
+                                       std::to_string(p.head_dim));
     }
     return FA_OK;
 }
@@ -1167,7 +1220,8 @@ int fa_flash_fwd(const fa_params* params, void* stream) {
         return fail(FA_EINVAL, "flash_fwd: seqlen * head_dim must be below 2^31");
     }
     fa_tile_info t{};
-    fa::tile_of(p.head_dim, p.causal != 0, p.variant, p.seqlen, &t);
+    fa::tile_of(p.head_dim, p.causal != 0, p.variant, p.seqlen,
+                static_cast<int64_t>(p.batch) * p.heads, &t);
     const int64_t blocks = static_cast<int64_t>(p.batch) * p.heads *
                            ((static_cast<int64_t>(p.seqlen) + t.block_q - 1) / t.block_q);
     if (blocks > INT32_MAX) {
@@ -1188,13 +1242,12 @@ int fa_flash_fwd(const fa_params* params, void* stream) {
     if (scale_log2 < 1.17549435e-38F) scale_log2 = 1.17549435e-38F;
 
     auto s = static_cast<hipStream_t>(stream);
-    if (fa::short_causal(p.head_dim, p.causal != 0, p.variant, p.seqlen)) {
-        return fa::launch<fa::OptD128CausalShort, true>(p, s, scale_log2, negate_q);
-    }
-    if (p.variant == FA_VARIANT_BASELINE) {
-        return fa::dispatch<fa::BaseSet>(p, s, scale_log2, negate_q);
-    }
-    return fa::dispatch<fa::OptSet>(p, s, scale_log2, negate_q);
+    const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
+    return fa::with_row(fa::tile_id(p.head_dim, p.causal != 0, p.variant, p.seqlen, bh),
+                        [&](auto row) {
+        using R = decltype(row);
+        return fa::launch<typename R::T, R::CAUSAL>(p, s, scale_log2, negate_q);
+    });
 }
 
 }  // extern "C"

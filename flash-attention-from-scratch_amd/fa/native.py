@@ -55,8 +55,7 @@ def lib() -> ctypes.CDLL:
     so.fa_flash_fwd.restype = ctypes.c_int
     so.fa_last_error.argtypes = []
     so.fa_last_error.restype = ctypes.c_char_p
-    so.fa_tile_config.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-                                  ctypes.POINTER(FaTileInfo)]
+    so.fa_tile_config.argtypes = [ctypes.POINTER(FaParams), ctypes.POINTER(FaTileInfo)]
     so.fa_tile_config.restype = ctypes.c_int
     so.fa_version.argtypes = []
     so.fa_version.restype = ctypes.c_char_p
@@ -83,12 +82,12 @@ def flash_fwd(params: FaParams, stream: int | None = None) -> tuple[int, str]:
 
 
 def tile_config(head_dim: int, causal: bool, variant: str | int = "opt",
-                seqlen: int = 16384) -> dict:
-    """Tile the launcher uses for these arguments (fa_tile_config)."""
+                seqlen: int = 16384, batch: int = 1, heads: int = 16) -> dict:
+    """Tile fa_flash_fwd launches for these arguments (fa_tile_config)."""
     so = lib()
     info = FaTileInfo()
-    var = VARIANTS[variant] if isinstance(variant, str) else int(variant)
-    rc = so.fa_tile_config(head_dim, 1 if causal else 0, var, seqlen, ctypes.byref(info))
+    p = make_params(0, 0, 0, 0, batch, heads, seqlen, head_dim, 1.0, causal, variant)
+    rc = so.fa_tile_config(ctypes.byref(p), ctypes.byref(info))
     if rc != FA_OK:
         raise ValueError(so.fa_last_error().decode())
     return {"block_q": info.block_q, "block_k": info.block_k, "waves": info.waves,

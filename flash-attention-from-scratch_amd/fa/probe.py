@@ -87,7 +87,7 @@ def _run_clock(so, q, k, v, causal: bool, reps: int = 20):
         times.append(e0.elapsed_time(e1))
     buf = (ctypes.c_ulonglong * (65536 * 2))()
     so.fa_probe_clock_fetch(buf)
-    tile = native.tile_config(d, causal, "opt", n)
+    tile = native.tile_config(d, causal, "opt", n, b, h)
     n_wg = b * h * ((n + tile["block_q"] - 1) // tile["block_q"])
     arr = np.frombuffer(buf, dtype=np.uint64).reshape(65536, 2)[:n_wg].astype(np.float64)
     ghz = arr[:, 0] / (arr[:, 1] * 10.0)

@@ -11,6 +11,8 @@ Targets (outputs are git-ignored; they travel to the GPU box with the source tre
   geom    tests/geometry/libfa_geom.so   host build of the tile geometry, for the CPU tests
   probe   fa/libfa_probe.so, fa/libfa_hip_clock.so   measurement only (python -m fa.probe):
           MFMA power-ceiling probes, and the kernels with per-workgroup clock recording
+  dev     dev/fa_dev             standalone C++ driver (no Python) over the C ABI, for
+          rocprofv3 counter runs and tile tuning (dev/counters.sh, dev/tune.py)
 
 Counterpart of the reference's setup.py / CMakeLists.txt / Makefile build targets
 (setup.py:12-33, CMakeLists.txt:56-87, Makefile:21-32): the kernel library is compiled by
@@ -138,9 +140,16 @@ def build_probe() -> list[Path]:
     return [out, clock]
 
 
+def build_dev() -> Path:
+    src = PKG / "dev" / "fa_dev.cpp"
+    out = src.parent / "fa_dev"
+    _run([_hipcc(), *HIP_FLAGS, "-Wextra", f"-I{INCLUDE}", str(src), "-o", str(out), "-ldl"])
+    return out
+
+
 TARGETS = {"lib": build_lib, "ext": build_ext, "blocks": build_blocks, "oracle": build_oracle,
-           "geom": build_geom, "probe": build_probe}
-ALL = ("lib", "ext", "blocks", "oracle", "geom", "probe")
+           "geom": build_geom, "probe": build_probe, "dev": build_dev}
+ALL = ("lib", "ext", "blocks", "oracle", "geom", "probe", "dev")
 
 
 def build_all() -> None:

@@ -70,20 +70,19 @@ int fa_flash_fwd(const fa_params* params, void* stream);
  * valid until the next fa_* call on the same thread. */
 const char* fa_last_error(void);
 
-/* Tile geometry the launcher picks for (head_dim, causal, variant, seqlen): query rows per
- * workgroup, keys per tile, wavefronts per workgroup and LDS bytes per workgroup. The choice
- * depends on seqlen only for causal d=128 (short sequences get 128-row workgroups).
- * Host-only, touches no device. No counterpart function in the reference, whose tiles are
- * compile-time `using` lines (csrc/kernels/flash_fwd.cu:597-612); exported so that tests and
- * the benchmark can report and check the grid the kernel runs. */
+/* Tile geometry fa_flash_fwd launches for these parameters: query rows per workgroup, keys per
+ * tile, wavefronts per workgroup and LDS bytes per workgroup. The choice depends on variant,
+ * head_dim, causal, seqlen and batch * heads (small grids get smaller workgroups); the four
+ * pointers are not read. Host-only, touches no device. No counterpart function in the
+ * reference, whose tiles are compile-time `using` lines (csrc/kernels/flash_fwd.cu:597-612);
+ * exported so that tests and the benchmark can report and check the grid the kernel runs. */
 typedef struct fa_tile_info {
     int32_t block_q;       /* BR: query rows per workgroup                                     */
     int32_t block_k;       /* BC: key rows per K/V tile                                        */
     int32_t waves;         /* wavefronts (64 lanes) per workgroup                              */
     int32_t lds_bytes;     /* LDS per workgroup                                                */
 } fa_tile_info;
-int fa_tile_config(int32_t head_dim, int32_t causal, int32_t variant, int32_t seqlen,
-                   fa_tile_info* out);
+int fa_tile_config(const fa_params* params, fa_tile_info* out);
 
 /* Library version string, e.g. "fa_hip 0.1.0 gfx950". */
 const char* fa_version(void);

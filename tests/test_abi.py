@@ -98,24 +98,50 @@ def test_null_params_and_reserved_bytes():
     assert native.flash_fwd(p)[0] == native.FA_EINVAL
 
 
-def test_tile_config():
+def _tile(d, causal, var, n, b=16, h=32):
+    t = native.tile_config(d, causal, var, n, b, h)
+    return t["block_q"], t["block_k"], t["waves"], t["lds_bytes"]
+
+
+def test_tile_config_invariants():
     for d in (64, 128):
         for causal in (False, True):
             for var in ("baseline", "opt", "fp16acc"):
-              for n in (1, 2048, 2049, 16384):
-                t = native.tile_config(d, causal, var, n)
-                assert t["block_q"] == 32 * t["waves"]
-                assert t["block_k"] % 32 == 0
-                # two or three K/V tile buffers each, depending on the schedule
-                assert t["lds_bytes"] in (4 * t["block_k"] * 2 * d, 6 * t["block_k"] * 2 * d)
-                assert t["lds_bytes"] <= 160 * 1024
-    assert native.tile_config(64, False, "fp16acc") == native.tile_config(64, False, "opt")
-    # causal d=128: short sequences get 128-row workgroups, long ones the 256-row ping-pong tile
-    assert native.tile_config(128, True, "opt", 2048)["block_q"] == 128
-    assert native.tile_config(128, True, "opt", 2049)["block_q"] == 256
-    assert native.tile_config(128, False, "opt", 512)["block_q"] == 256
+                for n in (1, 1000, 2048, 2049, 3072, 3073, 4096, 4097, 8192, 8193, 16384):
+                    for b, h in ((1, 1), (2, 8), (16, 32)):
+                        bq, bk, waves, lds = _tile(d, causal, var, n, b, h)
+                        assert bq == 32 * waves and bk % 32 == 0
+                        # two or three K/V tile buffers each, depending on the schedule
+                        assert lds in (4 * bk * 2 * d, 6 * bk * 2 * d) and lds <= 64 * 1024
+                        assert _tile(d, causal, "fp16acc", n, b, h) == _tile(d, causal, "opt", n, b, h)
+
+
+def test_tile_config_rows():
+    """The opt rows by N for a large grid (16 x 32 heads), and the small-grid rows."""
+    pingpong64, simple64x8 = (256, 64, 8, 49152), (256, 64, 8, 32768)
+    assert _tile(64, False, "opt", 2048) == simple64x8
+    assert _tile(64, False, "opt", 2049) == pingpong64
+    assert _tile(64, True, "opt", 4096) == simple64x8
+    assert _tile(64, True, "opt", 4097) == (128, 32, 4, 16384)         # pipelined
+    assert _tile(64, True, "opt", 8192) == (128, 32, 4, 16384)
+    assert _tile(64, True, "opt", 8193) == pingpong64
+    assert _tile(128, False, "opt", 512) == (256, 32, 8, 49152)        # ping-pong at every N
+    assert _tile(128, True, "opt", 3072) == (128, 32, 4, 32768)        # simple, 4 waves
+    assert _tile(128, True, "opt", 3073) == (256, 32, 8, 49152)
+    # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> 4-wave tiles
+    assert _tile(64, True, "opt", 1000, 2, 8) == (128, 64, 4, 32768)   # pipelined, BC=64
+    assert _tile(64, False, "opt", 256, 1, 4) == (128, 64, 4, 32768)
+    assert _tile(128, False, "opt", 16384, 1, 3) == (128, 64, 4, 65536)
+    assert _tile(128, False, "opt", 16384, 1, 4) == (256, 32, 8, 49152)  # 4 * 64 = 256 WGs
+    for n in (1, 5000, 16384):
+        assert _tile(64, n > 1, "baseline", n) == (128, 64, 4, 32768)
+
+
+def test_tile_config_errors():
     with pytest.raises(ValueError, match="seqlen"):
         native.tile_config(128, True, "opt", 0)
+    with pytest.raises(ValueError, match="positive"):
+        native.tile_config(128, True, "opt", 64, 0, 1)
     with pytest.raises(ValueError, match="head_dim"):
         native.tile_config(96, False)
     with pytest.raises(ValueError, match="variant"):

@@ -59,17 +59,6 @@ def test_matches_reference(n, d, causal, variant):
     _close(out, orc.attention_fp32(q, k, v, causal=causal))
 
 
-# Causal d=128 switches from 128-row workgroups to the 256-row ping-pong tile above N = 2048:
-# both sides of the switch, with ragged last query and key tiles on the long side.
-@pytest.mark.parametrize("n", [2047, 2048, 2049, 2300, 3001])
-def test_causal_d128_tile_switch(n):
-    from fa import native
-
-    print(f"case n={n} tile={native.tile_config(128, True, 'opt', n)}", flush=True)
-    q, k, v = _qkv(1, 2, n, 128, seed=7)
-    _close(_fa().forward(q, k, v, causal=True), orc.attention_fp32(q, k, v, causal=True))
-
-
 @pytest.mark.parametrize("b,h", [(1, 1), (3, 5), (8, 16)])
 def test_batch_heads(b, h):
     q, k, v = _qkv(b, h, 300, 64, seed=1)

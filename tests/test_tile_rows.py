@@ -1,0 +1,108 @@
+"""GPU: every row of the tile table against the CPU oracle, and both sides of every switch.
+
+The launcher picks a tile from (variant, head_dim, causal, N, B*H) (csrc/flash_fwd.hip, tile
+table). Each case here first checks, through fa_tile_config, that its shape selects the row it
+is meant to cover, then compares fa.forward with the fp32 oracle on a few (b, h) slices (the
+first, the last and one in between) with the north-star tolerance. Sequence lengths are
+ragged (not multiples of the tile) wherever a row allows it.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import ATOL, RTOL
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+
+
+def _check(b, h, n, d, causal, want, seed=11):
+    import fa
+    from fa import native
+
+    tile = native.tile_config(d, causal, "opt", n, b, h)
+    got = (tile["block_q"], tile["block_k"], tile["waves"], tile["lds_bytes"])
+    print(f"case B={b} H={h} N={n} d={d} causal={causal} tile={got}", flush=True)
+    assert got == want, (got, want)
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    out = fa.forward(q.cuda(), k.cuda(), v.cuda(), causal=causal).cpu()
+    for bi, hi in {(0, 0), (b // 2, h // 2), (b - 1, h - 1)}:
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+
+
+PP128 = (256, 32, 8, 49152)      # ping-pong, d=128
+PP64 = (256, 64, 8, 49152)       # ping-pong, d=64
+SIMPLE64X8 = (256, 64, 8, 32768)
+PIPE64 = (128, 32, 4, 16384)
+SIMPLE128X4 = (128, 32, 4, 32768)
+SMALL64 = (128, 64, 4, 32768)    # pipelined, BC=64
+SMALL128 = (128, 64, 4, 65536)   # simple, BC=64
+
+ROWS = [
+    # (B, H, N, d, causal, expected tile)
+    (1, 3, 1000, 64, False, SMALL64),
+    (2, 8, 1000, 64, True, SMALL64),          # the benchmark's ragged config
+    (1, 2, 1500, 128, False, SMALL128),
+    (1, 2, 1500, 128, True, SMALL128),
+    (4, 16, 1000, 64, False, SIMPLE64X8),
+    (1, 32, 2500, 64, False, PP64),
+    (4, 16, 1000, 64, True, SIMPLE64X8),
+    (1, 16, 5000, 64, True, PIPE64),
+    (1, 8, 8500, 64, True, PP64),
+    (4, 16, 1000, 128, False, PP128),
+    (4, 16, 1000, 128, True, SIMPLE128X4),
+    (1, 16, 4000, 128, True, PP128),
+]
+
+
+@pytest.mark.parametrize("b,h,n,d,causal,want", ROWS)
+def test_row(b, h, n, d, causal, want):
+    _check(b, h, n, d, causal, want)
+
+
+SWITCHES = [
+    (1, 32, 2048, 64, False, SIMPLE64X8), (1, 32, 2049, 64, False, PP64),
+    (1, 16, 4096, 64, True, SIMPLE64X8), (1, 16, 4097, 64, True, PIPE64),
+    (1, 8, 8192, 64, True, PIPE64), (1, 8, 8193, 64, True, PP64),
+    (1, 24, 3072, 128, True, SIMPLE128X4), (1, 24, 3073, 128, True, PP128),
+    # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
+    (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
+]
+
+
+@pytest.mark.parametrize("b,h,n,d,causal,want", SWITCHES)
+def test_switch(b, h, n, d, causal, want):
+    _check(b, h, n, d, causal, want, seed=12)
+
+
+@pytest.mark.parametrize("n", [1, 17, 65, 257, 1000])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_edge_lengths_large_grid(n, d, causal):
+    """The reference's edge lengths (tests/test_flash_fwd.py:27) on a grid large enough for the
+    main rows (B*H = 256, so never the small-grid row)."""
+    import fa
+    from fa import native
+
+    b, h = 16, 16
+    tile = native.tile_config(d, causal, "opt", n, b, h)
+    print(f"case B={b} H={h} N={n} d={d} causal={causal} tile={tile}", flush=True)
+    assert tile["waves"] == 8 or (d == 128 and causal)
+    g = torch.Generator().manual_seed(n + d)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    out = fa.forward(q.cuda(), k.cuda(), v.cuda(), causal=causal).cpu()
+    for bi, hi in {(0, 0), (7, 9), (15, 15)}:
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
