@@ -974,8 +974,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 // (FA2-paper shapes, B*N = 16k tokens): short sequences favour 256-row workgroups with the
 // simple schedule (less pipeline prologue and epilogue per workgroup, fewer diagonal tiles
 // on the ping-pong's masked path), long ones the ping-pong or pipelined schedules. Small grids
-// (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000) take 4-wave tiles, so
-// that each wave gets a SIMD of its own on twice as many CUs. Each entry is
+// (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000) take 2- or 4-wave
+// pipelined tiles, which spread the waves over more CUs, one per SIMD. Each entry is
 // "BC, NW, LAZY, SCHED" and can be overridden at build time with -DFA_<NAME>="..." (the
 // counterpart of bench/tune.sh, which rewrites the `using` lines with sed); so can each
 // threshold (a row applies while N <= its FA_*_MAX_N).
@@ -986,10 +986,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 #define FA_BASE_D128 64, 4, false, SIMPLE
 #endif
 #ifndef FA_OPT_D64_SMALL
-#define FA_OPT_D64_SMALL 64, 4, true, PIPE
+#define FA_OPT_D64_SMALL 64, 2, true, PIPE
 #endif
 #ifndef FA_OPT_D128_SMALL
-#define FA_OPT_D128_SMALL 64, 4, true, SIMPLE
+#define FA_OPT_D128_SMALL 32, 4, true, PIPE
 #endif
 #ifndef FA_OPT_D64_SHORT
 #define FA_OPT_D64_SHORT 64, 8, true, SIMPLE

@@ -128,10 +128,11 @@ def test_tile_config_rows():
     assert _tile(128, False, "opt", 512) == (256, 32, 8, 49152)        # ping-pong at every N
     assert _tile(128, True, "opt", 3072) == (128, 32, 4, 32768)        # simple, 4 waves
     assert _tile(128, True, "opt", 3073) == (256, 32, 8, 49152)
-    # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> 4-wave tiles
-    assert _tile(64, True, "opt", 1000, 2, 8) == (128, 64, 4, 32768)   # pipelined, BC=64
-    assert _tile(64, False, "opt", 256, 1, 4) == (128, 64, 4, 32768)
-    assert _tile(128, False, "opt", 16384, 1, 3) == (128, 64, 4, 65536)
+    # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> 2- or 4-wave pipelined tiles
+    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 2, 32768)
+    assert _tile(64, False, "opt", 256, 1, 4) == (64, 64, 2, 32768)
+    assert _tile(128, False, "opt", 16384, 1, 3) == (128, 32, 4, 32768)
+    assert _tile(128, True, "opt", 16384, 1, 3) == (128, 32, 4, 32768)
     assert _tile(128, False, "opt", 16384, 1, 4) == (256, 32, 8, 49152)  # 4 * 64 = 256 WGs
     for n in (1, 5000, 16384):
         assert _tile(64, n > 1, "baseline", n) == (128, 64, 4, 32768)

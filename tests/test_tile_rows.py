@@ -46,8 +46,8 @@ PP64 = (256, 64, 8, 49152)       # ping-pong, d=64
 SIMPLE64X8 = (256, 64, 8, 32768)
 PIPE64 = (128, 32, 4, 16384)
 SIMPLE128X4 = (128, 32, 4, 32768)
-SMALL64 = (128, 64, 4, 32768)    # pipelined, BC=64
-SMALL128 = (128, 64, 4, 65536)   # simple, BC=64
+SMALL64 = (64, 64, 2, 32768)     # pipelined, 2 waves, BC=64
+SMALL128 = (128, 32, 4, 32768)   # pipelined, 4 waves, BC=32
 
 ROWS = [
     # (B, H, N, d, causal, expected tile)
