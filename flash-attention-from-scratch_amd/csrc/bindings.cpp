@@ -1,5 +1,7 @@
-// PyTorch (ROCm) binding `fa._C.forward`: checks tensors, allocates O, and calls the C ABI of
-// libfa_hip.so (include/fa_hip.h) on the current HIP stream of torch.
+// PyTorch (ROCm) binding `fa._C`: checks tensors, allocates O (and the LSE or the split-KV
+// workspace where asked), and calls the C ABI of libfa_hip.so (include/fa_hip.h) on the current
+// HIP stream of torch. `forward` mirrors the reference binding; `forward_lse` and
+// `forward_splitkv` are additions of this library (no reference counterpart).
 //
 // Same signature, defaults and error conditions as the reference binding
 // (csrc/bindings.cpp:28-73): RuntimeError with the words "CUDA", "float16", "contiguous",
@@ -27,9 +29,7 @@ uint8_t parse_variant(const std::string& name) {
     TORCH_CHECK(false, "variant must be 'opt', 'fp16acc' or 'baseline', got '", name, "'");
 }
 
-torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
-                      bool causal, std::optional<double> softmax_scale,
-                      const std::string& variant) {
+void check_qkv(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v) {
     for (const auto* t : {&q, &k, &v}) {
         TORCH_CHECK(t->is_cuda(), "q, k, v must be CUDA (HIP) tensors");
         TORCH_CHECK(t->scalar_type() == torch::kHalf, "q, k, v must be float16");
@@ -40,13 +40,11 @@ torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torc
                 "q, k, v must have the same shape");
     TORCH_CHECK(q.device() == k.device() && q.device() == v.device(),
                 "q, k, v must be on the same device");
-    const uint8_t var = parse_variant(variant);
+}
 
-    // torch-ROCm tags HIP devices as DeviceType::CUDA; the masquerading guard and stream
-    // accessors are its HIP implementations for that device type.
-    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    auto o = torch::empty_like(q);
-
+fa_params make_params(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                      const torch::Tensor& o, bool causal, std::optional<double> softmax_scale,
+                      uint8_t variant) {
     const auto head_dim = q.size(3);
     fa_params p{};
     p.q = q.data_ptr();
@@ -61,16 +59,74 @@ torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torc
     p.softmax_scale = static_cast<float>(
         softmax_scale.value_or(1.0 / std::sqrt(static_cast<double>(head_dim))));
     p.causal = causal ? 1 : 0;
-    p.variant = var;
+    p.variant = variant;
+    return p;
+}
 
+void check_rc(int rc) {
+    if (rc == FA_EINVAL) throw std::invalid_argument(fa_last_error());
+    if (rc != FA_OK) throw std::runtime_error(fa_last_error());
+}
+
+hipStream_t stream_of(const torch::Tensor& q) {
+    return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
+}
+
+torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                      bool causal, std::optional<double> softmax_scale,
+                      const std::string& variant) {
+    check_qkv(q, k, v);
+    const uint8_t var = parse_variant(variant);
+    // torch-ROCm tags HIP devices as DeviceType::CUDA; the masquerading guard and stream
+    // accessors are its HIP implementations for that device type.
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto o = torch::empty_like(q);
+    const fa_params p = make_params(q, k, v, o, causal, softmax_scale, var);
     // N = 0 (or any empty dimension) returns an empty output without a launch
     // (csrc/bindings.cpp:60-62).
     if (q.numel() == 0) return o;
-    const int rc = fa_flash_fwd(
-        &p, c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream());
-    if (rc == FA_EINVAL) throw std::invalid_argument(fa_last_error());
-    if (rc != FA_OK) throw std::runtime_error(fa_last_error());
+    check_rc(fa_flash_fwd(&p, stream_of(q)));
     return o;
+}
+
+// (O, LSE): LSE [B, H, N] fp32, natural log of each row's sum of exp(scale * q.k).
+std::tuple<torch::Tensor, torch::Tensor> forward_lse(const torch::Tensor& q,
+                                                     const torch::Tensor& k,
+                                                     const torch::Tensor& v, bool causal,
+                                                     std::optional<double> softmax_scale,
+                                                     const std::string& variant) {
+    check_qkv(q, k, v);
+    const uint8_t var = parse_variant(variant);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto o = torch::empty_like(q);
+    auto lse = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(torch::kFloat));
+    const fa_params p = make_params(q, k, v, o, causal, softmax_scale, var);
+    if (q.numel() == 0) return {o, lse};
+    check_rc(fa_flash_fwd_lse(&p, lse.data_ptr<float>(), stream_of(q)));
+    return {o, lse};
+}
+
+// Split-KV forward (num_splits 0 = automatic); the fp32 workspace comes from torch's caching
+// allocator and lives until the kernels that use it have run (stream-ordered reuse).
+std::tuple<torch::Tensor, torch::Tensor> forward_splitkv(const torch::Tensor& q,
+                                                         const torch::Tensor& k,
+                                                         const torch::Tensor& v, bool causal,
+                                                         std::optional<double> softmax_scale,
+                                                         int64_t num_splits) {
+    check_qkv(q, k, v);
+    TORCH_CHECK(num_splits >= 0 && num_splits <= INT32_MAX, "num_splits must be >= 0");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    auto o = torch::empty_like(q);
+    auto lse = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(torch::kFloat));
+    fa_params p = make_params(q, k, v, o, causal, softmax_scale, FA_VARIANT_OPT);
+    if (q.numel() == 0) return {o, lse};
+    fa_splitkv_info info{};
+    check_rc(fa_splitkv_plan(&p, static_cast<int32_t>(num_splits), &info));
+    auto ws = torch::empty({static_cast<int64_t>(info.workspace_bytes / 4)},
+                           q.options().dtype(torch::kFloat));
+    check_rc(fa_flash_fwd_splitkv(&p, lse.data_ptr<float>(), static_cast<int32_t>(num_splits),
+                                  ws.data_ptr(), info.workspace_bytes, stream_of(q)));
+    return {o, lse};
 }
 
 }  // namespace
@@ -80,5 +136,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("forward", &forward, "FlashAttention forward: O = softmax(Q K^T * scale) V",
           py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal") = false,
           py::arg("softmax_scale") = py::none(), py::arg("variant") = "opt");
+    m.def("forward_lse", &forward_lse, "forward that also returns the row log-sum-exp [B, H, N]",
+          py::arg("q"), py::arg("k"), py::arg("v"), py::arg("causal") = false,
+          py::arg("softmax_scale") = py::none(), py::arg("variant") = "opt");
+    m.def("forward_splitkv", &forward_splitkv,
+          "split-KV forward for small grids; returns (O, LSE)", py::arg("q"), py::arg("k"),
+          py::arg("v"), py::arg("causal") = false, py::arg("softmax_scale") = py::none(),
+          py::arg("num_splits") = 0);
     m.def("version", []() { return std::string(fa_version()); });
 }

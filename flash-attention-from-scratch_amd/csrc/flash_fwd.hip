@@ -28,6 +28,7 @@
 //     N-1 and the clamped rows are never stored.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -67,6 +68,8 @@ __device__ unsigned long long g_fa_clock[65536][2];
 
 namespace fa {
 namespace {
+
+constexpr float kLn2 = 0.693147180559945309F;  // converts base-2 LSEs to natural log
 
 using namespace fa::dev;
 namespace g = fa::geom;
@@ -308,14 +311,24 @@ __device__ __forceinline__ void pv_frags(const f16x8 (&vf)[T::NB][2][T::DB],
             for (int db = 0; db < T::DB; ++db) oacc[db] = mfma32(vf[nb][h][db], p[nb][h], oacc[db]);
 }
 
+// Base-2 log-sum-exp of the row's scaled scores, m + log2(l): the lane's running max m (the
+// reference its exponentials were taken against) and the row sum l of both wave halves. l >= 1
+// whenever the row saw a key (the key that set m contributed exp2(0)); -inf for a row that saw
+// none (a split whose keys are all masked for it).
+__device__ __forceinline__ float row_lse2(float m_run, float l_tot) {
+    return l_tot > 0.0F ? m_run + __builtin_amdgcn_logf(l_tot) : -INFINITY;
+}
+
 // O = acc / l as fp16 (RNE) for the lane's query row, if it is < n. The lane holds feature
-// columns 32*db + 8*rq + 4*(lane/32) + 0..3: one 8-byte store each.
+// columns 32*db + 8*rq + 4*(lane/32) + 0..3: one 8-byte store each. If lse_h is not null, the
+// row's natural-log LSE (log of the sum of exp(scale * q.k) over its keys) goes to lse_h[qrow].
 template <class T>
-__device__ __forceinline__ void store_o(f16* oh, int qrow, int n, int lane, float l_run,
-                                        const f32x16 (&oacc)[T::DB]) {
+__device__ __forceinline__ void store_o(f16* oh, float* lse_h, int qrow, int n, int lane,
+                                        float m_run, float l_run, const f32x16 (&oacc)[T::DB]) {
     const float l_tot = sum_xor32(l_run);
     const float inv = (l_tot > 0.0F) ? (1.0F / l_tot) : 0.0F;
     if (qrow >= n) return;
+    if (lse_h != nullptr && lane < 32) lse_h[qrow] = row_lse2(m_run, l_tot) * kLn2;
     f16* dst = oh + static_cast<size_t>(qrow) * T::D + 4 * (lane >> 5);
 #pragma unroll
     for (int db = 0; db < T::DB; ++db)
@@ -327,32 +340,66 @@ __device__ __forceinline__ void store_o(f16* oh, int qrow, int n, int lane, floa
         }
 }
 
+// Split-KV partial result of the lane's query row, if it is < n: O_s = acc / l in fp32 (16-byte
+// stores) and the base-2 LSE of the split's keys, for the combine kernel.
+template <class T>
+__device__ __forceinline__ void store_partial(float* op, float* lp, int qrow, int n, int lane,
+                                              float m_run, float l_run,
+                                              const f32x16 (&oacc)[T::DB]) {
+    const float l_tot = sum_xor32(l_run);
+    const float inv = (l_tot > 0.0F) ? (1.0F / l_tot) : 0.0F;
+    if (qrow >= n) return;
+    if (lane < 32) lp[qrow] = row_lse2(m_run, l_tot);
+    float* dst = op + static_cast<size_t>(qrow) * T::D + 4 * (lane >> 5);
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+            const f32x16& a = oacc[db];
+            *reinterpret_cast<f32x4*>(dst + 32 * db + 8 * rq) =
+                f32x4{a[4 * rq] * inv, a[4 * rq + 1] * inv, a[4 * rq + 2] * inv,
+                      a[4 * rq + 3] * inv};
+        }
+}
+
 // ---- kernel, simple schedule (the "baseline" build) -----------------------------------------
 // Per tile: barrier, prefetch tile j+1, then S = QK^T, softmax, O += PV in sequence.
-template <class T, bool CAUSAL>
+// SPLIT (split-KV): block id = split * (B*H*query blocks) + work item; the workgroup runs key
+// tiles [split * tiles_per_split, +tiles_per_split) of its query block and writes the partial
+// O and LSE of each row to o_part / lse_part (layout [split][b*h][n][d] and [split][b*h][n]);
+// a workgroup whose range is empty exits at once (the combine kernel never reads it).
+template <class T, bool CAUSAL, bool SPLIT = false>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
-    f16* __restrict__ o, int n, int bh_count, int n_qblocks, float scale_log2, int negate_q) {
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
+    float* __restrict__ lse_part) {
     __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
-    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const int items = bh_count * n_qblocks;
+    const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
+    const g::Work w = g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                                 n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const f16* kh = k + head;
     const f16* vh = v + head;
     const int q0 = w.qb * T::BR;
     const int qw = q0 + wave * 32;       // first query of this wave
     const int qrow = qw + (lane & 31);   // this lane's query
-    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const int n_all = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const int j_begin = SPLIT ? split * tiles_per_split : 0;
+    const int n_tiles = SPLIT ? min(n_all, j_begin + tiles_per_split) : n_all;
+    if (j_begin >= n_tiles) return;  // workgroup-uniform: empty split
 
     // LDS: [K0 | K1 | V0 | V1]; buffer b of K at b*TILE_BYTES, of V at (2+b)*TILE_BYTES.
     auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
     auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
 
     const TileDma<T> dma(wave, lane);
-    load_tile<T>(kh, 0, n, kbuf(0), dma);
-    load_tile<T>(vh, 0, n, vbuf(0), dma);
+    load_tile<T>(kh, j_begin * T::BC, n, kbuf(j_begin & 1), dma);
+    load_tile<T>(vh, j_begin * T::BC, n, vbuf(j_begin & 1), dma);
     f16x8 qf[T::KK];
     load_q<T>(q + head, qrow, n, lane, negate_q, qf);
     const Frag<T> fr(lane);
@@ -363,7 +410,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     float m_run = -INFINITY;  // running max of this lane's query, log2 domain (scaled)
     float l_run = 0.0F;       // this lane's partial row sum (its 16 keys of each 32-key block)
 
-    for (int j = 0; j < n_tiles; ++j) {
+    for (int j = j_begin; j < n_tiles; ++j) {
         wait_vmem();
         __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
         if (j + 1 < n_tiles) {
@@ -382,7 +429,49 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         if (rescale) rescale_o<T>(oacc, alpha);
         pv_tile<T>(vbuf(j & 1), fr, p, oacc);
     }
-    store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+    if constexpr (SPLIT) {
+        const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
+        store_partial<T>(o_part + part * n * T::D, lse_part + part * n, qrow, n, lane, m_run,
+                         l_run, oacc);
+    } else {
+        store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
+                   m_run, l_run, oacc);
+    }
+}
+
+// Split-KV combine: for each row, LSE = log2-sum-exp2 of the splits' base-2 LSEs, and
+// O = sum_s 2^(lse_s - LSE) O_s. Splits past a causal row block's last key tile were never
+// run and are not read. One thread per 4 features of a row.
+template <int D>
+__global__ __launch_bounds__(256) void flash_fwd_combine(
+    const float* __restrict__ o_part, const float* __restrict__ lse_part, f16* __restrict__ o,
+    float* __restrict__ lse, int n, int bh_count, int n_splits, int tiles_per_split, int causal,
+    int block_q, int block_k) {
+    constexpr int TPR = D / 4;  // threads per row
+    const long long row = static_cast<long long>(blockIdx.x) * (256 / TPR) + threadIdx.x / TPR;
+    if (row >= static_cast<long long>(bh_count) * n) return;
+    const int c = 4 * (threadIdx.x % TPR);
+    const int i = static_cast<int>(row % n);
+    int splits = n_splits;
+    if (causal) {
+        const int kv_end = min(n, (i / block_q + 1) * block_q);
+        splits = min(n_splits, g::ceil_div(g::ceil_div(kv_end, block_k), tiles_per_split));
+    }
+    const size_t plane = static_cast<size_t>(bh_count) * n;  // rows per split
+    float m = -INFINITY;
+    for (int s = 0; s < splits; ++s) m = fmaxf(m, lse_part[s * plane + row]);
+    float wsum = 0.0F;
+    f32x4 acc{};
+    for (int s = 0; s < splits; ++s) {
+        const float wgt = exp2_fast(lse_part[s * plane + row] - m);
+        const f32x4 x = *reinterpret_cast<const f32x4*>(o_part + (s * plane + row) * D + c);
+        wsum += wgt;
+        acc += wgt * x;
+    }
+    const float inv = 1.0F / wsum;  // >= 1: the split holding the row's max weighs 1
+    *reinterpret_cast<f16x4*>(o + row * D + c) = pack4(acc[0] * inv, acc[1] * inv, acc[2] * inv,
+                                                       acc[3] * inv);
+    if (lse != nullptr && c == 0) lse[row] = (m + __builtin_amdgcn_logf(wsum)) * kLn2;
 }
 
 // Scheduler pattern: N times {one MFMA, then up to VALU_PER VALU instructions}. Masks of
@@ -578,7 +667,9 @@ __device__ __forceinline__ void general_tiles(
 template <class T, bool CAUSAL>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
-    f16* __restrict__ o, int n, int bh_count, int n_qblocks, float scale_log2, int negate_q) {
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
+    float* /*lse_part*/) {
     // Four separate LDS objects (K and V, two buffers each): with the buffer known at compile
     // time, the compiler can tell that a DMA refill and a fragment read touch different
     // objects and adds no wait between them.
@@ -688,7 +779,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     vb[1] = v_lds1;
     general_tiles<T, CAUSAL, 2>(j, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma, fr, qf, s,
                                 oacc, scale_log2, m_run, l_run);
-    store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+    store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
+               m_run, l_run, oacc);
     FA_CLOCK_END();
 }
 
@@ -812,7 +904,9 @@ __device__ __forceinline__ void matrix_phase(const f16x8 (&kf)[T::NB][T::KK],
 template <class T, bool CAUSAL>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
-    f16* __restrict__ o, int n, int bh_count, int n_qblocks, float scale_log2, int negate_q) {
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
+    float* /*lse_part*/) {
     static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
@@ -963,7 +1057,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     vb[2] = v_lds2;
     general_tiles<T, CAUSAL, 3>(n_steady, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma,
                                 fr, qf, s, oacc, scale_log2, m_run, l_run);
-    store_o<T>(o + head, qrow, n, lane, l_run, oacc);
+    store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
+               m_run, l_run, oacc);
     FA_CLOCK_END();
 }
 
@@ -1115,8 +1210,29 @@ int fail(int code, const std::string& msg) {
     return code;
 }
 
-template <class T, bool CAUSAL>
-int launch(const fa_params& p, hipStream_t stream, float scale_log2, int negate_q) {
+// Scale handling shared by every entry point. scale * log2(e) is folded into one FMA per score.
+// A negative scale is applied by negating Q (exact in fp16) so the kernel's row max can use
+// scale > 0; a zero scale becomes the smallest normal float, which leaves every exp2 argument at
+// exactly 0 after rounding but keeps masked scores at -inf (0 * -inf would be NaN).
+struct Scale {
+    float log2e_scaled;
+    int negate_q;
+};
+Scale scale_of(float softmax_scale) {
+    Scale r{softmax_scale, 0};
+    if (softmax_scale < 0.0F) {
+        r.log2e_scaled = -softmax_scale;
+        r.negate_q = 1;
+    }
+    r.log2e_scaled *= 1.44269504088896340736F;
+    if (r.log2e_scaled < 1.17549435e-38F) r.log2e_scaled = 1.17549435e-38F;
+    return r;
+}
+
+// One launch of kernel T (SPLIT: the split-KV partial pass over n_splits * items workgroups).
+template <class T, bool CAUSAL, bool SPLIT = false>
+int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_splits = 1,
+           int tiles_per_split = 0, float* o_part = nullptr, float* lse_part = nullptr) {
     const int n_qblocks = g::ceil_div(p.seqlen, T::BR);
     int n = p.seqlen;
     int bh = p.batch * p.heads;
@@ -1125,10 +1241,17 @@ int launch(const fa_params& p, hipStream_t stream, float scale_log2, int negate_
     const auto* vp = static_cast<const f16*>(p.v);
     auto* op = static_cast<f16*>(p.o);
     int nqb = n_qblocks;
-    void* args[] = {&qp, &kp, &vp, &op, &n, &bh, &nqb, &scale_log2, &negate_q};
-    const dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh));
+    float scale_log2 = sc.log2e_scaled;
+    int negate_q = sc.negate_q;
+    void* args[] = {&qp, &kp, &vp, &op, &lse, &n, &bh, &nqb, &scale_log2, &negate_q,
+                    &tiles_per_split, &o_part, &lse_part};
+    const dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh) *
+                    static_cast<unsigned>(n_splits));
     const void* fn;
-    if constexpr (T::SCHED == PINGPONG) {
+    if constexpr (SPLIT) {
+        static_assert(T::SCHED == SIMPLE, "split-KV runs the simple schedule");
+        fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
+    } else if constexpr (T::SCHED == PINGPONG) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
     } else if constexpr (T::SCHED == PIPE) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pipelined<T, CAUSAL>);
@@ -1143,6 +1266,99 @@ int launch(const fa_params& p, hipStream_t stream, float scale_log2, int negate_
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
+
+// ---- split-KV ---------------------------------------------------------------------------------
+// Tile of the split-KV partial pass (simple schedule; each workgroup runs a bounded key range,
+// so there is no long steady state for the pipelined schedules to win back their prologue).
+#ifndef FA_SPLIT_D64
+#define FA_SPLIT_D64 64, 4, true, SIMPLE
+#endif
+#ifndef FA_SPLIT_D128
+#define FA_SPLIT_D128 64, 4, true, SIMPLE
+#endif
+#ifndef FA_SPLIT_TARGET_WGS
+#define FA_SPLIT_TARGET_WGS 1024  // non-empty partial workgroups the automatic plan aims for
+#endif
+#ifndef FA_SPLIT_MIN_TILES
+#define FA_SPLIT_MIN_TILES 4  // key tiles per split at least
+#endif
+using SplitD64 = Tile<64, FA_SPLIT_D64>;
+using SplitD128 = Tile<128, FA_SPLIT_D128>;
+
+struct SplitPlan {
+    int n_splits;
+    int tiles_per_split;
+    int block_q;
+    int block_k;
+    uint64_t workspace_bytes;
+};
+
+// Splits the key tiles of every query block into ranges of tiles_per_split tiles. With
+// requested == 0 the range length is the total number of (query block, key tile) pairs over
+// FA_SPLIT_TARGET_WGS (at least FA_SPLIT_MIN_TILES), so that about that many workgroups have
+// work; otherwise the longest query block's tiles are cut into `requested` ranges. Workspace:
+// fp32 O and LSE per split and row.
+SplitPlan split_plan(const fa_params& p, int requested) {
+    const int br = p.head_dim == 64 ? SplitD64::BR : SplitD128::BR;
+    const int bc = p.head_dim == 64 ? SplitD64::BC : SplitD128::BC;
+    const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
+    const int nqb = g::ceil_div(p.seqlen, br);
+    const int max_tiles = g::ceil_div(p.seqlen, bc);
+    int tps;
+    if (requested > 0) {
+        tps = g::ceil_div(max_tiles, min(requested, max_tiles));
+    } else {
+        int64_t pairs = 0;
+        for (int qb = 0; qb < nqb; ++qb) {
+            pairs += g::num_kv_tiles(p.seqlen, qb * br, br, bc, p.causal != 0);
+        }
+        pairs *= bh;
+        const int64_t want = (pairs + FA_SPLIT_TARGET_WGS - 1) / FA_SPLIT_TARGET_WGS;
+        tps = static_cast<int>(std::min<int64_t>(std::max<int64_t>(FA_SPLIT_MIN_TILES, want),
+                                                 max_tiles));
+    }
+    SplitPlan sp{};
+    sp.tiles_per_split = tps;
+    sp.n_splits = g::ceil_div(max_tiles, tps);
+    sp.block_q = br;
+    sp.block_k = bc;
+    sp.workspace_bytes = static_cast<uint64_t>(sp.n_splits) * bh * p.seqlen * (p.head_dim + 1) * 4;
+    return sp;
+}
+
+template <int D>
+int combine(const fa_params& p, const SplitPlan& sp, const float* o_part, const float* lse_part,
+            float* lse, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(p.batch) * p.heads * p.seqlen;
+    constexpr int ROWS_PER_BLOCK = 256 / (D / 4);
+    const auto blocks = static_cast<unsigned>((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
+    auto* op = static_cast<f16*>(p.o);
+    int n = p.seqlen, bh = p.batch * p.heads, ns = sp.n_splits, tps = sp.tiles_per_split;
+    int causal = p.causal, bq = sp.block_q, bk = sp.block_k;
+    void* args[] = {&o_part, &lse_part, &op, &lse, &n, &bh, &ns, &tps, &causal, &bq, &bk};
+    const hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(&flash_fwd_combine<D>),
+                                           dim3(blocks), dim3(256), args, 0, stream);
+    if (err != hipSuccess) {
+        return fail(FA_EHIP, std::string("flash_fwd_splitkv: HIP launch failed: ") +
+                                 hipGetErrorString(err));
+    }
+    return FA_OK;
+}
+
+template <class T>
+int splitkv(const fa_params& p, float* lse, const SplitPlan& sp, void* workspace, Scale sc,
+            hipStream_t stream) {
+    auto* o_part = static_cast<float*>(workspace);
+    float* lse_part = o_part + static_cast<size_t>(sp.n_splits) * p.batch * p.heads * p.seqlen *
+                                   T::D;
+    const int rc = p.causal
+                       ? launch<T, true, true>(p, nullptr, stream, sc, sp.n_splits,
+                                               sp.tiles_per_split, o_part, lse_part)
+                       : launch<T, false, true>(p, nullptr, stream, sc, sp.n_splits,
+                                                sp.tiles_per_split, o_part, lse_part);
+    if (rc != FA_OK) return rc;
+    return combine<T::D>(p, sp, o_part, lse_part, lse, stream);
+}
 
 bool tile_of(int head_dim, bool causal, int variant, int seqlen, int64_t bh, fa_tile_info* out) {
     if (head_dim != 64 && head_dim != 128) return false;
@@ -1189,65 +1405,114 @@ int fa_tile_config(const fa_params* params, fa_tile_info* out) {
 // Argument checks follow csrc/kernels/flash_fwd.cu:626-651 (same conditions and message
 // keywords), extended with the checks a C caller needs (NULL pointers, reserved bytes,
 // non-finite scale, 32-bit index limits of this kernel).
-int fa_flash_fwd(const fa_params* params, void* stream) {
+static int validate(const fa_params* params, const char* who) {
     using fa::fail;
-    fa::g_last_error.clear();
-    if (params == nullptr) return fail(FA_EINVAL, "flash_fwd: params must not be NULL");
+    const std::string w = std::string(who) + ": ";
+    if (params == nullptr) return fail(FA_EINVAL, w + "params must not be NULL");
     const fa_params& p = *params;
     if (p.batch <= 0 || p.heads <= 0 || p.seqlen <= 0) {
-        return fail(FA_EINVAL, "flash_fwd: batch, heads and seqlen must be positive");
+        return fail(FA_EINVAL, w + "batch, heads and seqlen must be positive");
     }
     if (p.head_dim != 64 && p.head_dim != 128) {
-        return fail(FA_EINVAL,
-                    "flash_fwd: head_dim must be 64 or 128, got " + std::to_string(p.head_dim));
+        return fail(FA_EINVAL, w + "head_dim must be 64 or 128, got " + std::to_string(p.head_dim));
     }
-    if (p.variant > FA_VARIANT_FP16ACC) return fail(FA_EINVAL, "flash_fwd: unknown variant");
+    if (p.variant > FA_VARIANT_FP16ACC) return fail(FA_EINVAL, w + "unknown variant");
     if (p.causal > 1 || p.reserved[0] != 0 || p.reserved[1] != 0) {
-        return fail(FA_EINVAL, "flash_fwd: causal must be 0 or 1 and reserved bytes zero");
+        return fail(FA_EINVAL, w + "causal must be 0 or 1 and reserved bytes zero");
     }
     if (p.q == nullptr || p.k == nullptr || p.v == nullptr || p.o == nullptr) {
-        return fail(FA_EINVAL, "flash_fwd: q, k, v and o must be non-null");
+        return fail(FA_EINVAL, w + "q, k, v and o must be non-null");
     }
     if (!fa::aligned16(p.q) || !fa::aligned16(p.k) || !fa::aligned16(p.v) ||
         !fa::aligned16(p.o)) {
-        return fail(FA_EINVAL, "flash_fwd: tensors must be 16-byte aligned (16-byte loads)");
+        return fail(FA_EINVAL, w + "tensors must be 16-byte aligned (16-byte loads)");
     }
-    if (!std::isfinite(p.softmax_scale)) {
-        return fail(FA_EINVAL, "flash_fwd: softmax_scale must be finite");
-    }
+    if (!std::isfinite(p.softmax_scale)) return fail(FA_EINVAL, w + "softmax_scale must be finite");
     // Offsets inside one head are 32-bit; the grid is one-dimensional.
     if (static_cast<int64_t>(p.seqlen) * p.head_dim > INT32_MAX) {
-        return fail(FA_EINVAL, "flash_fwd: seqlen * head_dim must be below 2^31");
+        return fail(FA_EINVAL, w + "seqlen * head_dim must be below 2^31");
     }
-    fa_tile_info t{};
-    fa::tile_of(p.head_dim, p.causal != 0, p.variant, p.seqlen,
-                static_cast<int64_t>(p.batch) * p.heads, &t);
+    // The smallest workgroup has 64 query rows: this bounds the grid of every tile.
     const int64_t blocks = static_cast<int64_t>(p.batch) * p.heads *
-                           ((static_cast<int64_t>(p.seqlen) + t.block_q - 1) / t.block_q);
+                           ((static_cast<int64_t>(p.seqlen) + 63) / 64);
     if (blocks > INT32_MAX) {
-        return fail(FA_EINVAL, "flash_fwd: batch * heads * query blocks exceeds the grid limit");
+        return fail(FA_EINVAL, w + "batch * heads * query blocks exceeds the grid limit");
     }
+    return FA_OK;
+}
 
-    // scale * log2(e), folded into one FMA per score. A negative scale is applied by negating Q
-    // (exact in fp16) so the kernel's row max can use scale > 0; a zero scale becomes the
-    // smallest normal float, which leaves every exp2 argument at exactly 0 after rounding but
-    // keeps masked scores at -inf (0 * -inf would be NaN).
-    float scale = p.softmax_scale;
-    int negate_q = 0;
-    if (scale < 0.0F) {
-        scale = -scale;
-        negate_q = 1;
-    }
-    float scale_log2 = scale * 1.44269504088896340736F;
-    if (scale_log2 < 1.17549435e-38F) scale_log2 = 1.17549435e-38F;
-
+static int run(const fa_params& p, float* lse, void* stream) {
+    const fa::Scale sc = fa::scale_of(p.softmax_scale);
     auto s = static_cast<hipStream_t>(stream);
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
     return fa::with_row(fa::tile_id(p.head_dim, p.causal != 0, p.variant, p.seqlen, bh),
                         [&](auto row) {
         using R = decltype(row);
-        return fa::launch<typename R::T, R::CAUSAL>(p, s, scale_log2, negate_q);
+        return fa::launch<typename R::T, R::CAUSAL>(p, lse, s, sc);
     });
+}
+
+int fa_flash_fwd(const fa_params* params, void* stream) {
+    fa::g_last_error.clear();
+    const int rc = validate(params, "flash_fwd");
+    return rc != FA_OK ? rc : run(*params, nullptr, stream);
+}
+
+int fa_flash_fwd_lse(const fa_params* params, float* lse, void* stream) {
+    fa::g_last_error.clear();
+    const int rc = validate(params, "flash_fwd_lse");
+    if (rc != FA_OK) return rc;
+    if (lse == nullptr || (reinterpret_cast<uintptr_t>(lse) & 3U) != 0) {
+        return fa::fail(FA_EINVAL, "flash_fwd_lse: lse must be a non-null, 4-byte aligned float*");
+    }
+    return run(*params, lse, stream);
+}
+
+int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info* out) {
+    fa::g_last_error.clear();
+    if (out == nullptr) return fa::fail(FA_EINVAL, "fa_splitkv_plan: out must not be NULL");
+    if (params == nullptr) return fa::fail(FA_EINVAL, "fa_splitkv_plan: params must not be NULL");
+    const fa_params& p = *params;
+    if (p.batch <= 0 || p.heads <= 0 || p.seqlen <= 0) {
+        return fa::fail(FA_EINVAL, "fa_splitkv_plan: batch, heads and seqlen must be positive");
+    }
+    if (p.head_dim != 64 && p.head_dim != 128) {
+        return fa::fail(FA_EINVAL, "fa_splitkv_plan: head_dim must be 64 or 128, got " +
+                                       std::to_string(p.head_dim));
+    }
+    if (num_splits < 0) return fa::fail(FA_EINVAL, "fa_splitkv_plan: num_splits must be >= 0");
+    const fa::SplitPlan sp = fa::split_plan(p, num_splits);
+    *out = fa_splitkv_info{sp.n_splits, sp.tiles_per_split, sp.block_q, sp.block_k,
+                           sp.workspace_bytes};
+    return FA_OK;
+}
+
+int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits,
+                         void* workspace, uint64_t workspace_bytes, void* stream) {
+    fa::g_last_error.clear();
+    int rc = validate(params, "flash_fwd_splitkv");
+    if (rc != FA_OK) return rc;
+    const fa_params& p = *params;
+    if (num_splits < 0) return fa::fail(FA_EINVAL, "flash_fwd_splitkv: num_splits must be >= 0");
+    if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3U) != 0) {
+        return fa::fail(FA_EINVAL, "flash_fwd_splitkv: lse must be 4-byte aligned");
+    }
+    const fa::SplitPlan sp = fa::split_plan(p, num_splits);
+    if (static_cast<int64_t>(p.batch) * p.heads * fa::g::ceil_div(p.seqlen, sp.block_q) *
+            sp.n_splits > INT32_MAX) {
+        return fa::fail(FA_EINVAL, "flash_fwd_splitkv: splits * query blocks exceed the grid limit");
+    }
+    if (workspace == nullptr || !fa::aligned16(workspace)) {
+        return fa::fail(FA_EINVAL, "flash_fwd_splitkv: workspace must be non-null and 16-byte aligned");
+    }
+    if (workspace_bytes < sp.workspace_bytes) {
+        return fa::fail(FA_EINVAL, "flash_fwd_splitkv: workspace too small: need " +
+                                       std::to_string(sp.workspace_bytes) + " bytes");
+    }
+    const fa::Scale sc = fa::scale_of(p.softmax_scale);
+    auto s = static_cast<hipStream_t>(stream);
+    return p.head_dim == 64 ? fa::splitkv<fa::SplitD64>(p, lse, sp, workspace, sc, s)
+                            : fa::splitkv<fa::SplitD128>(p, lse, sp, workspace, sc, s);
 }
 
 }  // extern "C"

@@ -52,4 +52,34 @@ def forward_variant(
     return _C.forward(q, k, v, causal, None, variant)
 
 
-__all__ = ["forward", "forward_variant", "attention_reference", "attention_naive_fp16"]
+def forward_lse(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    softmax_scale: float | None = None,
+    variant: str = "opt",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(O, LSE): O as `forward`, bitwise, and LSE[b, h, i] = log(sum_j exp(scale * q_i . k_j))
+    over the keys row i sees, fp32 [B, H, N]. Not in the reference package; the LSE is what
+    merging partial attention results (split-KV, context parallelism) needs."""
+    return _C.forward_lse(q, k, v, causal, softmax_scale, variant)
+
+
+def forward_splitkv(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    softmax_scale: float | None = None,
+    num_splits: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(O, LSE) computed split-KV: every query block's keys are cut into ranges processed by
+    separate workgroups and merged by their LSEs. For grids too small to fill the GPU (few
+    heads, long sequences). num_splits = 0 picks the ranges automatically. Matches `forward`
+    within fp32 rounding of the merge. Not in the reference package."""
+    return _C.forward_splitkv(q, k, v, causal, softmax_scale, num_splits)
+
+
+__all__ = ["forward", "forward_variant", "forward_lse", "forward_splitkv", "attention_reference",
+           "attention_naive_fp16"]

@@ -46,6 +46,18 @@ class FaTileInfo(ctypes.Structure):
     ]
 
 
+class FaSplitKvInfo(ctypes.Structure):
+    """struct fa_splitkv_info (include/fa_hip.h)."""
+
+    _fields_ = [
+        ("num_splits", ctypes.c_int32),
+        ("tiles_per_split", ctypes.c_int32),
+        ("block_q", ctypes.c_int32),
+        ("block_k", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_uint64),
+    ]
+
+
 @lru_cache(maxsize=1)
 def lib() -> ctypes.CDLL:
     if not LIB_PATH.exists():
@@ -53,6 +65,15 @@ def lib() -> ctypes.CDLL:
     so = ctypes.CDLL(str(LIB_PATH))
     so.fa_flash_fwd.argtypes = [ctypes.POINTER(FaParams), ctypes.c_void_p]
     so.fa_flash_fwd.restype = ctypes.c_int
+    so.fa_flash_fwd_lse.argtypes = [ctypes.POINTER(FaParams), ctypes.c_void_p, ctypes.c_void_p]
+    so.fa_flash_fwd_lse.restype = ctypes.c_int
+    so.fa_splitkv_plan.argtypes = [ctypes.POINTER(FaParams), ctypes.c_int32,
+                                   ctypes.POINTER(FaSplitKvInfo)]
+    so.fa_splitkv_plan.restype = ctypes.c_int
+    so.fa_flash_fwd_splitkv.argtypes = [ctypes.POINTER(FaParams), ctypes.c_void_p,
+                                        ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint64,
+                                        ctypes.c_void_p]
+    so.fa_flash_fwd_splitkv.restype = ctypes.c_int
     so.fa_last_error.argtypes = []
     so.fa_last_error.restype = ctypes.c_char_p
     so.fa_tile_config.argtypes = [ctypes.POINTER(FaParams), ctypes.POINTER(FaTileInfo)]
@@ -78,6 +99,34 @@ def flash_fwd(params: FaParams, stream: int | None = None) -> tuple[int, str]:
     """Calls fa_flash_fwd; returns (status, fa_last_error())."""
     so = lib()
     rc = so.fa_flash_fwd(ctypes.byref(params), ctypes.c_void_p(stream or 0))
+    return rc, so.fa_last_error().decode()
+
+
+def flash_fwd_lse(params: FaParams, lse: int, stream: int | None = None) -> tuple[int, str]:
+    """Calls fa_flash_fwd_lse (lse: device address of a [B, H, N] fp32 buffer)."""
+    so = lib()
+    rc = so.fa_flash_fwd_lse(ctypes.byref(params), ctypes.c_void_p(lse),
+                             ctypes.c_void_p(stream or 0))
+    return rc, so.fa_last_error().decode()
+
+
+def splitkv_plan(params: FaParams, num_splits: int = 0) -> dict:
+    """fa_splitkv_plan: key ranges and workspace size of a split-KV call."""
+    so = lib()
+    info = FaSplitKvInfo()
+    rc = so.fa_splitkv_plan(ctypes.byref(params), num_splits, ctypes.byref(info))
+    if rc != FA_OK:
+        raise ValueError(so.fa_last_error().decode())
+    return {f: getattr(info, f) for f, _ in FaSplitKvInfo._fields_}
+
+
+def flash_fwd_splitkv(params: FaParams, lse: int | None, num_splits: int, workspace: int,
+                      workspace_bytes: int, stream: int | None = None) -> tuple[int, str]:
+    """Calls fa_flash_fwd_splitkv; returns (status, fa_last_error())."""
+    so = lib()
+    rc = so.fa_flash_fwd_splitkv(ctypes.byref(params), ctypes.c_void_p(lse or 0), num_splits,
+                                 ctypes.c_void_p(workspace), workspace_bytes,
+                                 ctypes.c_void_p(stream or 0))
     return rc, so.fa_last_error().decode()
 
 

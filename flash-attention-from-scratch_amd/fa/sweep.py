@@ -11,7 +11,7 @@ least 200 ms of calls), median of 20 to 200 calls within a 1.5 s budget (:112-12
 implementation's output is checked against fa's baseline kernel on the same inputs first
 (max |diff| < 2e-2, :128-132).
 
-Implementations: fa "opt", "fp16acc" and "baseline"; torch SDPA with the FLASH_ATTENTION and
+Implementations: fa "opt", "fp16acc" and "baseline", fa's split-KV forward; torch SDPA with the FLASH_ATTENTION and
 EFFICIENT_ATTENTION backends (the fused kernels of PyTorch-ROCm); and the naive fp16 matmul /
 softmax / matmul. The SDPA math backend is left out: its batched GEMMs take transposed views,
 which this GPU pool has seen fault. Inputs come from a seeded CPU generator.
@@ -45,6 +45,7 @@ def _impls():
 
     return {
         "fa opt": ours("opt"),
+        "fa splitkv": lambda q, k, v, causal: fa.forward_splitkv(q, k, v, causal=causal)[0],
         "fa fp16acc": ours("fp16acc"),
         "fa baseline": ours("baseline"),
         "sdpa flash": sdpa(SDPBackend.FLASH_ATTENTION),
@@ -91,18 +92,23 @@ def main(argv: list[str]) -> int:
     ap.add_argument("--causal", type=int, nargs="*", default=[0, 1])
     ap.add_argument("--tokens", type=int, default=16384, help="B * N")
     ap.add_argument("--hidden", type=int, default=2048, help="H * d")
+    ap.add_argument("--bh", type=int, nargs=2, default=None, metavar=("B", "H"),
+                    help="fixed batch and heads instead of the FA2-paper shapes")
+    ap.add_argument("--impls", nargs="*", default=None, help="subset of implementations")
     ap.add_argument("--csv", type=Path, default=Path("gpurun_out/sweep.csv"))
     ap.add_argument("--md", type=Path, default=None, help="also write a markdown table")
     args = ap.parse_args(argv)
 
     impls = _impls()
+    if args.impls:
+        impls = {k: v for k, v in impls.items() if k in args.impls}
     gpu = torch.cuda.get_device_name(0)
     print(f"GPU: {gpu}  torch {torch.__version__}  HIP {torch.version.hip}", flush=True)
     rows = []
     for d in args.d:
         for causal in map(bool, args.causal):
             for n in args.n:
-                b, h = max(1, args.tokens // n), args.hidden // d
+                b, h = args.bh if args.bh else (max(1, args.tokens // n), args.hidden // d)
                 g = torch.Generator().manual_seed(0)
                 q, k, v = (torch.randn(b, h, n, d, generator=g).half().cuda() for _ in range(3))
                 ref = fa.forward_variant(q, k, v, causal=causal, variant="baseline")

@@ -70,6 +70,36 @@ int fa_flash_fwd(const fa_params* params, void* stream);
  * valid until the next fa_* call on the same thread. */
 const char* fa_last_error(void);
 
+/* fa_flash_fwd that also writes the log-sum-exp of every row:
+ *   lse[b, h, i] = log(sum_j exp(softmax_scale * q_i . k_j))   (natural log, over visible keys)
+ * lse: [B, H, N] fp32, contiguous, 4-byte aligned. O is bitwise the output of fa_flash_fwd.
+ * The LSE is what merging partial attention results needs (split-KV below, sequence/context
+ * parallelism across GPUs) and what a backward pass recomputes P from. No counterpart in the
+ * reference, whose epilogue keeps only O (csrc/kernels/flash_fwd.cu:526-560). */
+int fa_flash_fwd_lse(const fa_params* params, float* lse, void* stream);
+
+/* Split-KV ("flash-decoding" style) forward for grids too small to fill the GPU (few heads,
+ * long sequences): the key tiles of every query block are cut into ranges, one workgroup per
+ * (query block, range) writes a partial O and LSE per row to the caller's workspace, and a
+ * second kernel merges them by their LSEs. Same results as fa_flash_fwd within fp32 rounding
+ * of the merge (not bitwise). No counterpart in the reference.
+ * fa_splitkv_plan reports the ranges and the workspace size for num_splits (0 = automatic:
+ * about a thousand workgroups with work); host-only. fa_flash_fwd_splitkv runs it: lse may be
+ * NULL; workspace must be 16-byte aligned and hold at least workspace_bytes of the plan for the
+ * same params and num_splits. Two launches on `stream`; allocates nothing. The variant field
+ * is checked but every variant runs the same split tile. */
+typedef struct fa_splitkv_info {
+    int32_t num_splits;       /* key ranges per query block (ranges past a causal block's last
+                                 key tile are skipped)                                        */
+    int32_t tiles_per_split;  /* key tiles per range                                          */
+    int32_t block_q;          /* query rows per workgroup of the partial pass                 */
+    int32_t block_k;          /* keys per tile                                                */
+    uint64_t workspace_bytes; /* num_splits * B * H * N * (D + 1) * 4                         */
+} fa_splitkv_info;
+int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info* out);
+int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits,
+                         void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Tile geometry fa_flash_fwd launches for these parameters: query rows per workgroup, keys per
  * tile, wavefronts per workgroup and LDS bytes per workgroup. The choice depends on variant,
  * head_dim, causal, seqlen and batch * heads (small grids get smaller workgroups); the four

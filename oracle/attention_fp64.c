@@ -10,6 +10,8 @@
  * p_j = exp(s_j - max_j s_j) / sum_j exp(s_j - max), o_i = sum_j p_j v_j.
  * Unlike the reference's versions the scale is a parameter (they fix 1/sqrt(d)), so the
  * custom-scale path of the binding (csrc/bindings.cpp:55-56) can be checked as well.
+ * oracle_lse_rows gives the same rows' log-sum-exp, max_j s_j + log(sum_j exp(s_j - max)):
+ * the reference computes it only implicitly (its kernel keeps m and l, flash_fwd.cu:526-560).
  */
 #include <math.h>
 #include <stddef.h>
@@ -79,5 +81,38 @@ int oracle_attention_rows(const uint16_t* q, const uint16_t* k, const uint16_t* 
     }
     free(s);
     free(qi);
+    return 0;
+}
+
+/* Natural-log log-sum-exp of the scaled scores of rows rows[0..n_rows) of head `bh`:
+ * out[r] = max_j s_j + log(sum_j exp(s_j - max_j s_j)) over the visible keys. Returns 0 or -1. */
+int oracle_lse_rows(const uint16_t* q, const uint16_t* k, int64_t bh, int64_t n, int64_t d,
+                    double scale, int causal, const int64_t* rows, int64_t n_rows, double* out) {
+    if (n <= 0 || d <= 0 || n_rows < 0) return -1;
+    const size_t base = (size_t)bh * (size_t)n * (size_t)d;
+    double* s = (double*)malloc((size_t)n * sizeof(double));
+    if (s == NULL) return -1;
+    for (int64_t r = 0; r < n_rows; ++r) {
+        const int64_t i = rows[r];
+        if (i < 0 || i >= n) {
+            free(s);
+            return -1;
+        }
+        const int64_t kv_end = causal ? i + 1 : n;
+        double mx = -INFINITY;
+        for (int64_t j = 0; j < kv_end; ++j) {
+            double dot = 0.0;
+            for (int64_t c = 0; c < d; ++c) {
+                dot += oracle_half_to_double(q[base + (size_t)(i * d + c)]) *
+                       oracle_half_to_double(k[base + (size_t)(j * d + c)]);
+            }
+            s[j] = dot * scale;
+            if (s[j] > mx) mx = s[j];
+        }
+        double sum = 0.0;
+        for (int64_t j = 0; j < kv_end; ++j) sum += exp(s[j] - mx);
+        out[r] = mx + log(sum);
+    }
+    free(s);
     return 0;
 }

@@ -34,7 +34,8 @@ def _declared_functions():
 
 def test_library_exports_every_declared_function():
     names = _declared_functions()
-    assert {"fa_flash_fwd", "fa_last_error", "fa_tile_config", "fa_version"} <= set(names)
+    assert {"fa_flash_fwd", "fa_last_error", "fa_tile_config", "fa_version", "fa_flash_fwd_lse",
+            "fa_splitkv_plan", "fa_flash_fwd_splitkv"} <= set(names)
     so = native.lib()
     for name in names:
         assert hasattr(so, name), name
@@ -165,3 +166,54 @@ def test_extension_imports_and_rejects_host_tensors():
         fa.forward(q, q, q)
     with pytest.raises(RuntimeError, match="CUDA"):
         fa.forward_variant(q, q, q, variant="nope")
+
+
+# ---- LSE and split-KV entry points: host-side checks (all fail before any HIP call) ---------
+def test_lse_entry_rejects_bad_lse_pointer():
+    p = native.make_params(**GOOD)
+    assert native.flash_fwd_lse(p, 0) == (native.FA_EINVAL, native.flash_fwd_lse(p, 0)[1])
+    rc, msg = native.flash_fwd_lse(p, 0x1002)
+    assert rc == native.FA_EINVAL and "4-byte aligned" in msg
+    rc, msg = native.flash_fwd_lse(native.make_params(**{**GOOD, "head_dim": 96}), 0x1000)
+    assert rc == native.FA_EINVAL and "head_dim must be 64 or 128, got 96" in msg
+
+
+@pytest.mark.parametrize("b,h,n,d,causal", [(1, 2, 16384, 128, False), (1, 2, 16384, 128, True),
+                                            (2, 8, 1000, 64, True), (1, 1, 1, 64, False),
+                                            (16, 32, 2048, 64, True)])
+def test_splitkv_plan(b, h, n, d, causal):
+    p = native.make_params(**{**GOOD, "batch": b, "heads": h, "seqlen": n, "head_dim": d,
+                              "causal": causal})
+    bc = 64
+    max_tiles = -(-n // bc)
+    for req in (0, 1, 2, 3, 7, 100000):
+        plan = native.splitkv_plan(p, req)
+        ns, tps = plan["num_splits"], plan["tiles_per_split"]
+        assert plan["block_k"] == bc and plan["block_q"] == 128
+        assert ns * tps >= max_tiles > (ns - 1) * tps       # ranges cover the keys, none empty
+        assert plan["workspace_bytes"] == ns * b * h * n * (d + 1) * 4
+        if req:
+            assert ns <= req
+        else:
+            assert tps >= min(4, max_tiles)
+    if (b, h, n, d, causal) == (1, 2, 16384, 128, False):
+        # 2 heads x 128 query blocks x 256 key tiles / 1024 target workgroups = 64 tiles
+        assert native.splitkv_plan(p, 0)["tiles_per_split"] == 64
+
+
+def test_splitkv_entry_rejects_bad_workspace():
+    p = native.make_params(**{**GOOD, "heads": 2, "seqlen": 3000, "head_dim": 128})
+    need = native.splitkv_plan(p, 3)["workspace_bytes"]
+    rc, msg = native.flash_fwd_splitkv(p, None, 3, 0x10000, need - 1)
+    assert rc == native.FA_EINVAL and f"need {need} bytes" in msg
+    rc, msg = native.flash_fwd_splitkv(p, None, 3, 0, need)
+    assert rc == native.FA_EINVAL and "workspace must be non-null" in msg
+    rc, msg = native.flash_fwd_splitkv(p, None, 3, 0x10008, need)
+    assert rc == native.FA_EINVAL and "16-byte aligned" in msg
+    rc, msg = native.flash_fwd_splitkv(p, None, -1, 0x10000, need)
+    assert rc == native.FA_EINVAL and "num_splits" in msg
+    rc, msg = native.flash_fwd_splitkv(p, 0x1001, 3, 0x10000, need)
+    assert rc == native.FA_EINVAL and "lse must be 4-byte aligned" in msg
+    with pytest.raises(ValueError, match="num_splits"):
+        native.splitkv_plan(p, -2)
+
