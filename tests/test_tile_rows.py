@@ -106,3 +106,19 @@ def test_edge_lengths_large_grid(n, d, causal):
         sl = (slice(bi, bi + 1), slice(hi, hi + 1))
         ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("d,causal", [(64, False), (128, True)])
+def test_more_heads_than_the_reference_grid_limit(d, causal):
+    """B*H = 70000 > 65535, which the reference rejects (its grid.y is B*H,
+    csrc/kernels/flash_fwd.cu:571-572, 629-631); the 1-D grid here takes it."""
+    import fa
+
+    b, h, n = 70000, 1, 16
+    g = torch.Generator().manual_seed(70000 + d)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    out = fa.forward(q.cuda(), k.cuda(), v.cuda(), causal=causal).cpu()
+    for bi in (0, 35000, b - 1):
+        sl = (slice(bi, bi + 1), slice(0, 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
