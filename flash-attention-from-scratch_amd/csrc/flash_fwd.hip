@@ -61,9 +61,37 @@ __device__ unsigned long long g_fa_clock[65536][2];
             g_fa_clock[blockIdx.x][1] = fa_r1 - fa_r0;                    \
         }                                                                 \
     } while (0)
+// Ping-pong phase timing (same build): per wave, shader cycles summed over the steady tiles
+// for [0] issuing the softmax phase, [1] its end-of-phase wait and barrier, [2] issuing the
+// matrix phase, [3] its wait and barrier; [4] steady tiles, [5] cycles of the whole wave.
+// The stamps sit next to the phase-end waits, whose lgkmcnt(0) the s_memtime results need.
+__device__ unsigned long long g_fa_phase[8192][8][6];
+#define FA_PHASE_DECL()                                   \
+    unsigned long long fa_ph[6] = {0, 0, 0, 0, 0, 0};     \
+    const unsigned long long fa_pt0 = __builtin_amdgcn_s_memtime()
+#define FA_PHASE_T(var) const unsigned long long var = __builtin_amdgcn_s_memtime()
+#define FA_PHASE_TILE(ta, tb, tc, td, te) \
+    do {                                  \
+        fa_ph[0] += (tb) - (ta);          \
+        fa_ph[1] += (tc) - (tb);          \
+        fa_ph[2] += (td) - (tc);          \
+        fa_ph[3] += (te) - (td);          \
+        fa_ph[4] += 1;                    \
+    } while (0)
+#define FA_PHASE_STORE(wave, lane)                                               \
+    do {                                                                         \
+        fa_ph[5] = __builtin_amdgcn_s_memtime() - fa_pt0;                        \
+        if ((lane) == 0 && blockIdx.x < 8192) {                                  \
+            for (int fa_i = 0; fa_i < 6; ++fa_i) g_fa_phase[blockIdx.x][wave][fa_i] = fa_ph[fa_i]; \
+        }                                                                        \
+    } while (0)
 #else
 #define FA_CLOCK_BEGIN() static_cast<void>(0)
 #define FA_CLOCK_END() static_cast<void>(0)
+#define FA_PHASE_DECL() static_cast<void>(0)
+#define FA_PHASE_T(var) static_cast<void>(0)
+#define FA_PHASE_TILE(ta, tb, tc, td, te) static_cast<void>(0)
+#define FA_PHASE_STORE(wave, lane) static_cast<void>(0)
 #endif
 
 namespace fa {
@@ -375,6 +403,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
     float* __restrict__ lse_part) {
     __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+    FA_CLOCK_BEGIN();
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -437,6 +466,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
                    m_run, l_run, oacc);
     }
+    FA_CLOCK_END();
 }
 
 // Split-KV combine: for each row, LSE = log2-sum-exp2 of the splits' base-2 LSEs, and
@@ -976,6 +1006,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     f32x16 s[T::NB];
     if (n_act > 0) qk_tile<T>(kbuf(I0{}), fr, qf, s);
 
+    FA_PHASE_DECL();
     // The steady phases, compiled once per group so that every wait and refill of a wave is
     // unconditional code (the compiler then tracks exactly which DMA has landed).
     auto steady = [&](auto group) {
@@ -992,6 +1023,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
             end_phase<false>();
         }
         auto tile = [&](int jj, auto r) {
+            FA_PHASE_T(ta);
             constexpr int R = decltype(r)::value;  // jj % 3
             using Rj = std::integral_constant<int, R>;
             using Rj1 = std::integral_constant<int, (R + 1) % 3>;
@@ -1011,7 +1043,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
             // No branch here: the phase ends as soon as the softmax is issued, without waiting
             // for its results. The overflow test is taken at the start of the matrix phase,
             // before S is overwritten, when its flag has long been computed.
+            FA_PHASE_T(tb);
             end_phase<G == 1>();
+            FA_PHASE_T(tc);
             // matrix phase M_jj
             if (__builtin_expect(overflow, 0)) {  // rare: exact softmax of this tile, new max,
                 float alpha;                       // rescaled O
@@ -1028,7 +1062,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
                 }
             });
             __builtin_amdgcn_s_setprio(0);
+            FA_PHASE_T(td);
             end_phase<G == 0>();
+            FA_PHASE_T(te);
+            FA_PHASE_TILE(ta, tb, tc, td, te);
         };
         int jj = 0;
         for (; jj + 3 <= n_steady; jj += 3) {
@@ -1059,6 +1096,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
                                 fr, qf, s, oacc, scale_log2, m_run, l_run);
     store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
                m_run, l_run, oacc);
+    FA_PHASE_STORE(wave, lane);
     FA_CLOCK_END();
 }
 
@@ -1377,6 +1415,11 @@ extern "C" {
 // (65536 x 2 entries). Exists only in the clock-probe build.
 int fa_probe_clock_fetch(unsigned long long* host) {
     return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fa_clock), sizeof(g_fa_clock)));
+}
+
+// Copies the ping-pong phase sums of the last launch (8192 workgroups x 8 waves x 6) to `host`.
+int fa_probe_phase_fetch(unsigned long long* host) {
+    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fa_phase), sizeof(g_fa_phase)));
 }
 #endif
 

@@ -1,6 +1,6 @@
 """Power and clock measurements on MI355X (not part of the attention API).
 
-    PYTHONPATH=flash-attention-from-scratch_amd python3 -m fa.probe [ceiling] [clock] [busy]
+    PYTHONPATH=flash-attention-from-scratch_amd python3 -m fa.probe [ceiling] [clock] [busy] [phase]
 
 ceiling: TFLOPS and measured clock of pure v_mfma_f32_32x32x16_f16 streams on random fp16
          operands (8 waves per CU), alone and with the per-tile VALU work and LDS fragment reads
@@ -10,6 +10,9 @@ clock:   the clock the attention kernels themselves run at, and their shader cyc
          per-workgroup s_memtime / s_memrealtime recording).
 busy:    the same for cfg4's non-causal kernel with 16, 8, 4, 2 and 1 heads: with fewer busy CUs
          the clock rises at unchanged cycles per workgroup when chip power is the limit.
+phase:   the ping-pong kernel's steady state on cfg4, per wave group: shader cycles per tile spent
+         issuing the softmax phase and the matrix phase, and waiting at each phase's end
+         (s_memtime stamps at the phase-end waits of the clock-probe build).
 Prints one JSON line per measurement. Build first: fa_build.py --only probe.
 """
 
@@ -58,6 +61,7 @@ def _clock_lib():
     so.fa_flash_fwd.restype = ctypes.c_int
     so.fa_last_error.restype = ctypes.c_char_p
     so.fa_probe_clock_fetch.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
+    so.fa_probe_phase_fetch.argtypes = [ctypes.POINTER(ctypes.c_ulonglong)]
     return so
 
 
@@ -90,6 +94,7 @@ def _run_clock(so, q, k, v, causal: bool, reps: int = 20):
     tile = native.tile_config(d, causal, "opt", n, b, h)
     n_wg = b * h * ((n + tile["block_q"] - 1) // tile["block_q"])
     arr = np.frombuffer(buf, dtype=np.uint64).reshape(65536, 2)[:n_wg].astype(np.float64)
+    arr = arr[arr[:, 1] > 0]  # workgroups that recorded (e.g. not the empty split-KV ones)
     ghz = arr[:, 0] / (arr[:, 1] * 10.0)
     return statistics.median(times), float(np.median(ghz)), float(np.median(arr[:, 0])), n_wg
 
@@ -129,10 +134,37 @@ def busy() -> None:
                "cycles_per_workgroup_median": round(cyc)})
 
 
+def phase() -> None:
+    import numpy as np
+
+    from fa.configs import CONFIGS, make_inputs
+
+    so = _clock_lib()
+    cfg = CONFIGS["cfg4"]
+    q, k, v = make_inputs(cfg)
+    for causal in (False, True):
+        ms, ghz, _, n_wg = _run_clock(so, q, k, v, causal)
+        buf = (ctypes.c_ulonglong * (8192 * 8 * 6))()
+        so.fa_probe_phase_fetch(buf)
+        a = np.frombuffer(buf, dtype=np.uint64).reshape(8192, 8, 6)[:n_wg].astype(np.float64)
+        rec = {"probe": "pingpong_phases", "config": "cfg4", "causal": causal,
+               "median_ms": round(ms, 4), "clock_ghz_median": round(ghz, 3),
+               "tflops": round(cfg.flops(causal) / (ms * 1e-3) / 1e12, 1)}
+        for grp in (0, 1):
+            g = a[:, 4 * grp:4 * grp + 4]
+            tiles = g[:, :, 4]
+            for i, name in enumerate(("softmax_issue", "softmax_wait", "matrix_issue",
+                                      "matrix_wait")):
+                rec[f"group{grp}_{name}"] = round(float(np.mean(g[:, :, i][tiles > 0] /
+                                                                tiles[tiles > 0])), 1)
+        rec["mfma_cycles_per_tile_per_wave"] = 16 * 32
+        _emit(rec)
+
+
 def main(argv: list[str]) -> int:
-    what = argv or ["ceiling", "clock", "busy"]
+    what = argv or ["ceiling", "clock", "busy", "phase"]
     for w in what:
-        {"ceiling": ceiling, "clock": clock, "busy": busy}[w]()
+        {"ceiling": ceiling, "clock": clock, "busy": busy, "phase": phase}[w]()
     return 0
 
 
