@@ -111,7 +111,7 @@ namespace g = fa::geom;
 // Main-loop schedules: SIMPLE (flash_fwd_kernel), PIPE (flash_fwd_pipelined: QK of tile j+1
 // interleaved with the softmax of tile j in each wave), PINGPONG (flash_fwd_pingpong: two
 // groups of waves alternate between an MFMA-only phase and a softmax phase).
-enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2 };
+enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3 };
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
@@ -121,12 +121,13 @@ struct Tile {
     static constexpr bool LAZY = LAZY_;     // rescale O only when a row max grows by > 2^8
     static constexpr int SCHED = SCHED_;    // main-loop schedule (Sched)
     static constexpr int BR = 32 * NW;      // query rows per workgroup
-    static constexpr int THREADS = 64 * NW;
+    static constexpr int KS = SCHED == KSPLIT ? 2 : 1;  // waves per 32 query rows (key halves)
+    static constexpr int THREADS = 64 * NW * KS;
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
     static constexpr int NBUF = SCHED == PINGPONG ? 3 : 2;  // buffers each for K and V
-    static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES;
+    static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES * KS;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
     static constexpr int DB = D / 32;                  // 32-wide output blocks over D
@@ -351,9 +352,9 @@ __device__ __forceinline__ float row_lse2(float m_run, float l_tot) {
 // columns 32*db + 8*rq + 4*(lane/32) + 0..3: one 8-byte store each. If lse_h is not null, the
 // row's natural-log LSE (log of the sum of exp(scale * q.k) over its keys) goes to lse_h[qrow].
 template <class T>
-__device__ __forceinline__ void store_o(f16* oh, float* lse_h, int qrow, int n, int lane,
-                                        float m_run, float l_run, const f32x16 (&oacc)[T::DB]) {
-    const float l_tot = sum_xor32(l_run);
+__device__ __forceinline__ void store_o_tot(f16* oh, float* lse_h, int qrow, int n, int lane,
+                                            float m_run, float l_tot,
+                                            const f32x16 (&oacc)[T::DB]) {
     const float inv = (l_tot > 0.0F) ? (1.0F / l_tot) : 0.0F;
     if (qrow >= n) return;
     if (lse_h != nullptr && lane < 32) lse_h[qrow] = row_lse2(m_run, l_tot) * kLn2;
@@ -366,6 +367,14 @@ __device__ __forceinline__ void store_o(f16* oh, float* lse_h, int qrow, int n, 
             *reinterpret_cast<f16x4*>(dst + 32 * db + 8 * rq) = pack4(
                 a[4 * rq] * inv, a[4 * rq + 1] * inv, a[4 * rq + 2] * inv, a[4 * rq + 3] * inv);
         }
+}
+
+// Same, from the lane's partial row sum (its keys of each 32-key block; the two wave halves
+// hold the two halves of a row's keys).
+template <class T>
+__device__ __forceinline__ void store_o(f16* oh, float* lse_h, int qrow, int n, int lane,
+                                        float m_run, float l_run, const f32x16 (&oacc)[T::DB]) {
+    store_o_tot<T>(oh, lse_h, qrow, n, lane, m_run, sum_xor32(l_run), oacc);
 }
 
 // Split-KV partial result of the lane's query row, if it is < n: O_s = acc / l in fp32 (16-byte
@@ -502,6 +511,125 @@ __global__ __launch_bounds__(256) void flash_fwd_combine(
     *reinterpret_cast<f16x4*>(o + row * D + c) = pack4(acc[0] * inv, acc[1] * inv, acc[2] * inv,
                                                        acc[3] * inv);
     if (lse != nullptr && c == 0) lse[row] = (m + __builtin_amdgcn_logf(wsum)) * kLn2;
+}
+
+// ---- kernel, key-split schedule (small grids) --------------------------------------------------
+// Two waves per 32 query rows: wave w < NW takes the even key tiles of the query block and wave
+// w + NW the odd ones, each with its own running max, row sum and O (simple schedule per
+// tile); at the end the odd half hands (m, l, O) to the even half through LDS, which merges
+// them (O = 2^(m_a - m) O_a + 2^(m_b - m) O_b, l likewise) and stores. Twice the waves of the
+// simple schedule on the same grid, for grids too small to fill the GPU, with no workspace.
+template <class T, bool CAUSAL>
+__global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
+    float* /*lse_part*/) {
+    static_assert(T::KS == 2, "two key halves");
+    // Tiles: half h, buffer b: K at (2h + b) * 2 tiles, V right after. Reused by the merge.
+    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+    FA_CLOCK_BEGIN();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_uniform(threadIdx.x >> 6);
+    const int half = wave / T::NW;  // 0: even key tiles, 1: odd key tiles
+    const int wq = wave % T::NW;    // which 32 query rows
+    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
+    const f16* kh = k + head;
+    const f16* vh = v + head;
+    const int q0 = w.qb * T::BR;
+    const int qw = q0 + wq * 32;
+    const int qrow = qw + (lane & 31);
+    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const int n_steps = (n_tiles + 1) / 2;
+    auto kbuf = [&](int b) { return smem + (2 * half + b) * 2 * T::TILE_BYTES; };
+    auto vbuf = [&](int b) { return kbuf(b) + T::TILE_BYTES; };
+
+    const TileDma<T> dma(wq, lane);
+    if (half < n_tiles) {
+        load_tile<T>(kh, half * T::BC, n, kbuf(0), dma);
+        load_tile<T>(vh, half * T::BC, n, vbuf(0), dma);
+    }
+    f16x8 qf[T::KK];
+    load_q<T>(q + head, qrow, n, lane, negate_q, qf);
+    const Frag<T> fr(lane);
+
+    f32x16 oacc[T::DB];
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db) oacc[db] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0F;
+
+    for (int j = 0; j < n_steps; ++j) {
+        wait_vmem();
+        __syncthreads();  // step j's tiles are in LDS; step j-1's buffers are free
+        const int tn = 2 * (j + 1) + half;
+        if (tn < n_tiles) {
+            load_tile<T>(kh, tn * T::BC, n, kbuf((j + 1) & 1), dma);
+            load_tile<T>(vh, tn * T::BC, n, vbuf((j + 1) & 1), dma);
+        }
+        const int t = 2 * j + half;
+        const int kt = t * T::BC;
+        if (t >= n_tiles || qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) continue;
+        f32x16 s[T::NB];
+        qk_tile<T>(kbuf(j & 1), fr, qf, s);
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
+        f16x8 p[T::NB][2];
+        float alpha;
+        bool rescale;
+        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale_o<T>(oacc, alpha);
+        pv_tile<T>(vbuf(j & 1), fr, p, oacc);
+    }
+
+    // Merge through LDS: (m, l) of the odd half, then O one 32-column block at a time.
+    const float l_tot = sum_xor32(l_run);
+    float* ml = reinterpret_cast<float*>(smem);       // [NW][64][2]
+    float* ob = ml + T::NW * 128;                     // [NW][64][16]
+    const int slot = wq * 64 + lane;
+    wait_vmem();
+    __syncthreads();  // every wave is done with the tile buffers
+    if (half == 1) {
+        ml[2 * slot] = m_run;
+        ml[2 * slot + 1] = l_tot;
+    }
+    __syncthreads();
+    float m_new = m_run, wa = 1.0F, wb = 0.0F, l_new = l_tot;
+    if (half == 0) {
+        const float mb = ml[2 * slot];
+        const float lb = ml[2 * slot + 1];
+        m_new = fmaxf(m_run, mb);
+        // a half that saw no key has m = -inf and weighs 0; both -inf only for rows >= n
+        wa = m_run == -INFINITY ? 0.0F : exp2_fast(m_run - m_new);
+        wb = mb == -INFINITY ? 0.0F : exp2_fast(mb - m_new);
+        l_new = l_tot * wa + lb * wb;
+    }
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db) {
+        if (half == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) {
+                *reinterpret_cast<f32x4*>(ob + 16 * slot + r) =
+                    f32x4{oacc[db][r], oacc[db][r + 1], oacc[db][r + 2], oacc[db][r + 3]};
+            }
+        }
+        __syncthreads();
+        if (half == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 4) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(ob + 16 * slot + r);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) oacc[db][r + i] = oacc[db][r + i] * wa + x[i] * wb;
+            }
+        }
+        __syncthreads();
+    }
+    if (half == 0) {
+        store_o_tot<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n,
+                       lane, m_new, l_new, oacc);
+    }
+    FA_CLOCK_END();
 }
 
 // Scheduler pattern: N times {one MFMA, then up to VALU_PER VALU instructions}. Masks of
@@ -1107,8 +1235,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 // (FA2-paper shapes, B*N = 16k tokens): short sequences favour 256-row workgroups with the
 // simple schedule (less pipeline prologue and epilogue per workgroup, fewer diagonal tiles
 // on the ping-pong's masked path), long ones the ping-pong or pipelined schedules. Small grids
-// (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000) take 2- or 4-wave
-// pipelined tiles, which spread the waves over more CUs, one per SIMD. Each entry is
+// (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000) take the key-split
+// schedule with 64-row workgroups: two waves per 32 query rows, each on half the key tiles,
+// so the same grid keeps twice the SIMDs busy. Each entry is
 // "BC, NW, LAZY, SCHED" and can be overridden at build time with -DFA_<NAME>="..." (the
 // counterpart of bench/tune.sh, which rewrites the `using` lines with sed); so can each
 // threshold (a row applies while N <= its FA_*_MAX_N).
@@ -1119,10 +1248,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 #define FA_BASE_D128 64, 4, false, SIMPLE
 #endif
 #ifndef FA_OPT_D64_SMALL
-#define FA_OPT_D64_SMALL 64, 2, true, PIPE
+#define FA_OPT_D64_SMALL 64, 2, true, KSPLIT
 #endif
 #ifndef FA_OPT_D128_SMALL
-#define FA_OPT_D128_SMALL 32, 4, true, PIPE
+#define FA_OPT_D128_SMALL 32, 2, true, KSPLIT
 #endif
 #ifndef FA_OPT_D64_SHORT
 #define FA_OPT_D64_SHORT 64, 8, true, SIMPLE
@@ -1238,7 +1367,7 @@ decltype(auto) with_row(TileId id, F&& f) {
 
 template <class T>
 constexpr fa_tile_info info_of() {
-    return fa_tile_info{T::BR, T::BC, T::NW, T::LDS_BYTES};
+    return fa_tile_info{T::BR, T::BC, T::NW * T::KS, T::LDS_BYTES};
 }
 
 thread_local std::string g_last_error;
@@ -1291,6 +1420,8 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
         fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
     } else if constexpr (T::SCHED == PINGPONG) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
+    } else if constexpr (T::SCHED == KSPLIT) {
+        fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
     } else if constexpr (T::SCHED == PIPE) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pipelined<T, CAUSAL>);
     } else {

@@ -111,9 +111,11 @@ def test_tile_config_invariants():
                 for n in (1, 1000, 2048, 2049, 3072, 3073, 4096, 4097, 8192, 8193, 16384):
                     for b, h in ((1, 1), (2, 8), (16, 32)):
                         bq, bk, waves, lds = _tile(d, causal, var, n, b, h)
-                        assert bq == 32 * waves and bk % 32 == 0
-                        # two or three K/V tile buffers each, depending on the schedule
-                        assert lds in (4 * bk * 2 * d, 6 * bk * 2 * d) and lds <= 64 * 1024
+                        # 32 query rows per wave, or per pair of waves (key split)
+                        assert bq in (32 * waves, 16 * waves) and bk % 32 == 0
+                        # two or three K/V tile buffers each, per key half
+                        assert lds in (4 * bk * 2 * d, 6 * bk * 2 * d, 8 * bk * 2 * d)
+                        assert lds <= 64 * 1024
                         assert _tile(d, causal, "fp16acc", n, b, h) == _tile(d, causal, "opt", n, b, h)
 
 
@@ -129,11 +131,12 @@ def test_tile_config_rows():
     assert _tile(128, False, "opt", 512) == (256, 32, 8, 49152)        # ping-pong at every N
     assert _tile(128, True, "opt", 3072) == (128, 32, 4, 32768)        # simple, 4 waves
     assert _tile(128, True, "opt", 3073) == (256, 32, 8, 49152)
-    # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> 2- or 4-wave pipelined tiles
-    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 2, 32768)
-    assert _tile(64, False, "opt", 256, 1, 4) == (64, 64, 2, 32768)
-    assert _tile(128, False, "opt", 16384, 1, 3) == (128, 32, 4, 32768)
-    assert _tile(128, True, "opt", 16384, 1, 3) == (128, 32, 4, 32768)
+    # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
+    # two waves on each 32 rows)
+    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 4, 65536)
+    assert _tile(64, False, "opt", 256, 1, 4) == (64, 64, 4, 65536)
+    assert _tile(128, False, "opt", 16384, 1, 3) == (64, 32, 4, 65536)
+    assert _tile(128, True, "opt", 16384, 1, 3) == (64, 32, 4, 65536)
     assert _tile(128, False, "opt", 16384, 1, 4) == (256, 32, 8, 49152)  # 4 * 64 = 256 WGs
     for n in (1, 5000, 16384):
         assert _tile(64, n > 1, "baseline", n) == (128, 64, 4, 32768)

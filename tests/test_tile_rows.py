@@ -46,8 +46,8 @@ PP64 = (256, 64, 8, 49152)       # ping-pong, d=64
 SIMPLE64X8 = (256, 64, 8, 32768)
 PIPE64 = (128, 32, 4, 16384)
 SIMPLE128X4 = (128, 32, 4, 32768)
-SMALL64 = (64, 64, 2, 32768)     # pipelined, 2 waves, BC=64
-SMALL128 = (128, 32, 4, 32768)   # pipelined, 4 waves, BC=32
+SMALL64 = (64, 64, 4, 65536)     # key split: 64 rows, 2 x 2 waves, BC=64
+SMALL128 = (64, 32, 4, 65536)    # key split: 64 rows, 2 x 2 waves, BC=32
 
 ROWS = [
     # (B, H, N, d, causal, expected tile)
