@@ -19,6 +19,8 @@
 namespace {
 
 using namespace fa::dev;
+typedef unsigned uint4_t __attribute__((ext_vector_type(4)));
+typedef unsigned uint2_t __attribute__((ext_vector_type(2)));
 
 template <int VALU, int LDS>
 __global__ __launch_bounds__(512) void probe_kernel(const f16x8* __restrict__ src, float* out,
@@ -89,9 +91,102 @@ __global__ __launch_bounds__(512) void probe_kernel(const f16x8* __restrict__ sr
     }
 }
 
+// LDS read throughput alone: every wave of a 512-thread workgroup issues `iters` rounds of
+// 8 independent reads (MODE 0: ds_read_b128 with the K-fragment pattern, MODE 1:
+// ds_read_b64_tr_b16 with the V^T pattern), folding the results with one xor per read so
+// that nothing waits on a read before the next one issues. The addresses move every round
+// (the LDS contents never change, so repeated addresses would let the compiler fold reads).
+template <int MODE>
+__global__ __launch_bounds__(512) void probe_lds_kernel(float* out, unsigned long long* clk,
+                                                        int iters) {
+    __shared__ __attribute__((aligned(1024))) char lds[32768];
+    const int t = threadIdx.x;
+    for (int i = t; i < 32768 / 4; i += 512) reinterpret_cast<unsigned*>(lds)[i] = i * 2654435761U;
+    __syncthreads();
+    const int lane = t & 63;
+    const unsigned kbase = (lane & 31) * 256 + 16 * ((lane >> 5) ^ ((lane & 31) & 15));
+    const unsigned vbase = ((lane & 15) >> 2) * 256 + 8 * (lane & 3) + 64 * (lane >> 4);
+    unsigned acc = 0;
+    const unsigned long long s0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+        const unsigned shift = static_cast<unsigned>(it) * 272U;  // new addresses every round
+        if (MODE == 0) {
+            f32x4 r[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                r[k] = *reinterpret_cast<const f32x4*>(lds + ((kbase + k * 32 + shift) & 32752));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const auto u = __builtin_bit_cast(uint4_t, r[k]);
+                acc ^= u[0] ^ u[1] ^ u[2] ^ u[3];
+            }
+        } else {
+            f16x4 w[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) w[k] = lds_read_tr16(lds + ((vbase + k * 1024 + shift) & 32760));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const auto u = __builtin_bit_cast(uint2_t, w[k]);
+                acc ^= u[0] ^ u[1];
+            }
+        }
+    }
+    const unsigned long long s1 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    out[blockIdx.x * 512 + t] = static_cast<float>(acc);
+    if (t == 0) {
+        clk[blockIdx.x * 2] = s1 - s0;
+        clk[blockIdx.x * 2 + 1] = r1 - r0;
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+// LDS read probe: mode 0 = ds_read_b128, 1 = ds_read_b64_tr_b16; `blocks` workgroups of 8
+// waves, `iters` rounds of 8 reads per wave. *cycles: mean shader cycles per workgroup.
+int fa_probe_lds(int mode, int blocks, int iters, float* ms, double* ghz, double* cycles) {
+    if (blocks <= 0 || blocks > 65536 || iters <= 0 || mode < 0 || mode > 1) {
+        return static_cast<int>(hipErrorInvalidValue);
+    }
+    float* d = nullptr;
+    unsigned long long* c = nullptr;
+    hipError_t err = hipMalloc(&d, static_cast<size_t>(blocks) * 512 * sizeof(float));
+    if (err == hipSuccess) err = hipMalloc(&c, static_cast<size_t>(blocks) * 2 * sizeof(unsigned long long));
+    if (err != hipSuccess) return static_cast<int>(err);
+    auto launch = [&](int it) {
+        if (mode == 0) hipLaunchKernelGGL((probe_lds_kernel<0>), dim3(blocks), dim3(512), 0, 0, d, c, it);
+        else hipLaunchKernelGGL((probe_lds_kernel<1>), dim3(blocks), dim3(512), 0, 0, d, c, it);
+    };
+    hipEvent_t e0, e1;
+    (void)hipEventCreate(&e0);
+    (void)hipEventCreate(&e1);
+    launch(iters);
+    (void)hipEventRecord(e0, nullptr);
+    launch(iters);
+    (void)hipEventRecord(e1, nullptr);
+    err = hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(ms, e0, e1);
+    unsigned long long* hc = new unsigned long long[2 * static_cast<size_t>(blocks)];
+    (void)hipMemcpy(hc, c, static_cast<size_t>(blocks) * 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    double sg = 0.0;
+    double sc = 0.0;
+    for (int i = 0; i < blocks; ++i) {
+        sg += static_cast<double>(hc[2 * i]) / (static_cast<double>(hc[2 * i + 1]) * 10.0);
+        sc += static_cast<double>(hc[2 * i]);
+    }
+    *ghz = sg / blocks;
+    *cycles = sc / blocks;
+    delete[] hc;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipFree(d);
+    (void)hipFree(c);
+    return err == hipSuccess ? static_cast<int>(hipGetLastError()) : static_cast<int>(err);
+}
+
 
 // Runs the probe: `blocks` workgroups of 8 waves, `iters` iterations of 16 MFMAs per wave.
 // Returns the HIP status; *ms is the kernel time, *ghz the mean measured clock, *cycles the mean

@@ -964,6 +964,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
 #ifndef FA_PP_PRIO
 #define FA_PP_PRIO 1
 #endif
+#ifndef FA_PP_MASKED_STEADY
+#define FA_PP_MASKED_STEADY 1
+#endif
 
 // Scheduler pattern: N times {R DS reads, V VALU instructions} (sched_group_barrier masks
 // 0x100 DS read, 0x002 VALU | 0x400 transcendental).
@@ -1090,11 +1093,15 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
     const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
     // Steady tiles are the same for the whole workgroup (both groups must pass the same
-    // barriers): those wave 0, the one with the fewest, can take without a mask and with an
-    // active successor.
+    // barriers). With FA_PP_MASKED_STEADY every tile but the last runs in the steady phases,
+    // diagonal and tail tiles masked there (a wave whose rows are all left of a tile computes
+    // it to p = 0); otherwise only those that wave 0, the one with the fewest, can take
+    // without a mask and with an active successor.
     const int n_act0 = g::wave_active_tiles(n, q0, 32, T::BC, n_tiles, CAUSAL);
-    const int n_steady = max(0, min(g::wave_unmasked_tiles(n, q0, T::BC, n_act0, CAUSAL),
-                                    n_act0 - 1));
+    const int n_steady =
+        FA_PP_MASKED_STEADY ? max(0, n_tiles - 1)
+                            : max(0, min(g::wave_unmasked_tiles(n, q0, T::BC, n_act0, CAUSAL),
+                                         n_act0 - 1));
 
     // Buffer b (compile-time in the steady loop, so the compiler can tell the objects apart).
     auto kbuf = [&](auto b) {
@@ -1157,6 +1164,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
             using Rj1 = std::integral_constant<int, (R + 1) % 3>;
             using Rj2 = std::integral_constant<int, (R + 2) % 3>;
             // softmax phase S_jj
+            if (FA_PP_MASKED_STEADY && g::tile_needs_mask(n, jj * T::BC, T::BC, qw, CAUSAL)) {
+                mask_tile<T, CAUSAL>(s, jj * T::BC, n, qrow, lane);
+            }
             f16x8 kf[T::NB][T::KK];
             f16x8 vf[T::NB][2][T::DB];
             load_k_frags<T>(kbuf(Rj1{}), fr, kf);

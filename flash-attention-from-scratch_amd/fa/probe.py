@@ -53,6 +53,25 @@ def ceiling(blocks: int = 1024, iters: int = 2000) -> None:
                "cycles_per_16_mfma_per_simd": round(cyc.value / iters, 1)})
 
 
+def lds(blocks: int = 256, iters: int = 4000) -> None:
+    """LDS read throughput per CU for the two fragment-read instructions, alone."""
+    so = ctypes.CDLL(str(HERE / "libfa_probe.so"))
+    so.fa_probe_lds.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_double),
+                                ctypes.POINTER(ctypes.c_double)]
+    for mode, name, bytes_per_read in ((0, "ds_read_b128", 16), (1, "ds_read_b64_tr_b16", 8)):
+        ms, ghz, cyc = ctypes.c_float(), ctypes.c_double(), ctypes.c_double()
+        rc = so.fa_probe_lds(mode, blocks, iters, ctypes.byref(ms), ctypes.byref(ghz),
+                             ctypes.byref(cyc))
+        if rc != 0:
+            raise RuntimeError(f"fa_probe_lds failed with HIP status {rc}")
+        per_wg = 8 * 64 * 8 * bytes_per_read * iters  # waves x lanes x reads x bytes x rounds
+        # 256 workgroups of 8 waves: about one per CU, so this is bytes per CU cycle
+        _emit({"probe": "lds_read", "instruction": name,
+               "bytes_per_cycle_per_workgroup": round(per_wg / cyc.value, 1),
+               "clock_ghz": round(ghz.value, 3), "ms": round(ms.value, 3)})
+
+
 def _clock_lib():
     from fa import native
 
@@ -164,7 +183,7 @@ def phase() -> None:
 def main(argv: list[str]) -> int:
     what = argv or ["ceiling", "clock", "busy", "phase"]
     for w in what:
-        {"ceiling": ceiling, "clock": clock, "busy": busy, "phase": phase}[w]()
+        {"ceiling": ceiling, "clock": clock, "busy": busy, "phase": phase, "lds": lds}[w]()
     return 0
 
 
