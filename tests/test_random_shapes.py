@@ -1,0 +1,77 @@
+"""GPU: seeded random shapes and arguments against the CPU oracle.
+
+Forty draws (fixed seed, so the case list is the same on every run) of batch, heads, sequence
+length, head dim, causal, variant and softmax scale, with B*H*N small enough for the oracle but
+spread so that every tile row (small grid, simple, pipelined, ping-pong, key split) and both
+sides of the size thresholds come up. Each case checks fa.forward_variant against the fp32
+oracle on two (b, h) slices with the north-star tolerance, and fa.forward_lse's LSE against the
+oracle's LSE (2e-3 absolute).
+"""
+
+from __future__ import annotations
+
+import math
+import random
+
+import pytest
+import torch
+
+from conftest import ATOL, RTOL
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(count=40, seed=20261201):
+    rnd = random.Random(seed)
+    out = []
+    for i in range(count):
+        d = rnd.choice([64, 128])
+        n = rnd.choice([1, 7, 31, 64, 100, 255, 256, 257, 1000, 2047, 2049, 3073, 4097, 5000, 8193])
+        # half the draws on grids of at least 256 eight-wave workgroups (the large-grid rows),
+        # half below; at most 8M elements per tensor
+        blocks = (n + 255) // 256
+        bh_large = -(-256 // blocks)
+        if rnd.random() < 0.5 and bh_large * n * d <= 8 << 20:
+            bh = rnd.randint(bh_large, max(bh_large, min(2 * bh_large, (8 << 20) // (n * d))))
+        else:
+            bh = rnd.randint(1, max(1, min(bh_large - 1, (1 << 20) // (n * d) + 1)))
+        b = rnd.choice([x for x in (1, 2, 4) if bh % x == 0])
+        h = bh // b
+        causal = rnd.random() < 0.5
+        variant = rnd.choice(["opt", "opt", "fp16acc", "baseline"])
+        scale = rnd.choice([None, None, 0.05, 0.3, -0.2])
+        out.append((i, b, h, n, d, causal, variant, scale))
+    return out
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+
+
+@pytest.mark.parametrize("i,b,h,n,d,causal,variant,scale", _cases())
+def test_random_case(i, b, h, n, d, causal, variant, scale):
+    import fa
+    from fa import native
+
+    tile = native.tile_config(d, causal, variant, n, b, h)
+    print(f"case {i}: B={b} H={h} N={n} d={d} causal={causal} {variant} scale={scale} "
+          f"tile={tile}", flush=True)
+    g = torch.Generator().manual_seed(1000 + i)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    if scale is None:
+        out = fa.forward_variant(qc, kc, vc, causal=causal, variant=variant)
+    else:
+        out = fa._C.forward(qc, kc, vc, causal, scale, variant)
+    _, lse = fa.forward_lse(qc, kc, vc, causal=causal, softmax_scale=scale, variant=variant)
+    out, lse = out.cpu(), lse.cpu()
+    for bi, hi in {(0, 0), (b - 1, h - 1)}:
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal, scale=scale)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+        ref_lse = orc.lse_fp32(q[sl], k[sl], causal, scale)
+        torch.testing.assert_close(lse[sl], ref_lse, atol=2e-3, rtol=0)
+    assert math.isfinite(float(out.float().abs().max()))
