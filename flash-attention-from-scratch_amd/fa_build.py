@@ -70,11 +70,46 @@ def _hipcc() -> str:
     return str(ROCM / "bin" / "hipcc")
 
 
+def _kernel_resources(remarks: str) -> dict:
+    """Per-kernel VGPRs, AGPRs, scratch bytes per lane, occupancy (waves per SIMD) and LDS
+    bytes, from hipcc's -Rpass-analysis=kernel-resource-usage remarks."""
+    import re
+
+    out: dict = {}
+    name = None
+    fields = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch",
+              "Occupancy [waves/SIMD]": "occupancy", "LDS Size [bytes/block]": "lds"}
+    for line in remarks.splitlines():
+        m = re.search(r"remark: (.*?) \[-Rpass-analysis=kernel-resource-usage\]", line)
+        if not m:
+            continue
+        text = m.group(1).strip()
+        if text.startswith("Function Name: "):
+            name = text[len("Function Name: "):]
+            out[name] = {}
+        elif name is not None and ":" in text:
+            key, _, val = text.rpartition(":")
+            if key.strip() in fields and val.strip().lstrip("-").isdigit():
+                out[name][fields[key.strip()]] = int(val)
+    return out
+
+
 def build_lib(extra: list[str] | None = None) -> Path:
+    """Builds fa/libfa_hip.so and records each kernel's register, scratch, occupancy and LDS
+    use in fa/libfa_hip.resources.json (checked by tests/test_kernel_resources.py)."""
+    import json
+
     out = FA / "libfa_hip.so"
     cmd = [_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}",
-           str(CSRC / "flash_fwd.hip"), "-o", str(out), *(extra or [])]
-    _run(cmd)
+           "-Rpass-analysis=kernel-resource-usage", str(CSRC / "flash_fwd.hip"), "-o", str(out),
+           *(extra or [])]
+    print("+", " ".join(shlex.quote(c) for c in cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        err = "\n".join(ln for ln in res.stderr.splitlines() if "remark:" not in ln)
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    (FA / "libfa_hip.resources.json").write_text(
+        json.dumps(_kernel_resources(res.stderr), indent=1, sort_keys=True) + "\n")
     return out
 
 

@@ -1,0 +1,62 @@
+"""CPU: register, scratch and occupancy budget of every kernel in the built library.
+
+fa_build.py records hipcc's kernel-resource-usage remarks for libfa_hip.so in
+fa/libfa_hip.resources.json. The schedules are designed for a number of waves per SIMD
+(the ping-pong pairs two waves on a SIMD, the simple d=64 tile runs two 8-wave workgroups per
+CU, ...); a code change that makes the compiler spill or drop a kernel below its occupancy
+costs far more than any instruction it saves (an innocuous-looking early exit once cost the
+causal d=64 tile 30 VGPRs and half its occupancy). This test pins the budget.
+"""
+
+from __future__ import annotations
+
+import json
+import re
+from pathlib import Path
+
+import pytest
+
+RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" / "fa" / \
+    "libfa_hip.resources.json"
+TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
+SIMPLE, PIPE, PINGPONG, KSPLIT = 0, 1, 2, 3
+
+
+def _load():
+    if not RES.exists():
+        pytest.skip("library not built (fa_build.py --only lib)")
+    return json.loads(RES.read_text())
+
+
+def _min_occupancy(name: str) -> int:
+    if "flash_fwd_combine" in name:
+        return 4
+    d, bc, nw, _lazy, sched = (int(x) for x in TILE.search(name).groups())
+    if "flash_fwd_pingpong" in name:
+        return 2                      # waves w and w+4 share a SIMD
+    if "flash_fwd_ksplit" in name:
+        return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
+    if "flash_fwd_pipelined" in name:
+        return 3 if d == 64 else 1
+    assert "flash_fwd_kernel" in name and sched == SIMPLE
+    return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
+
+
+def test_every_kernel_is_recorded():
+    res = _load()
+    families = {k.split("INS0_")[0].split("ILi")[0] for k in res}
+    for f in ("flash_fwd_kernel", "flash_fwd_pingpong", "flash_fwd_pipelined", "flash_fwd_ksplit",
+              "flash_fwd_combine"):
+        assert any(f in x for x in families), f
+
+
+def test_no_kernel_spills_to_scratch():
+    for name, r in _load().items():
+        assert r.get("scratch", 0) == 0, (name, r)
+
+
+def test_kernels_keep_their_occupancy():
+    for name, r in _load().items():
+        want = _min_occupancy(name)
+        assert r["occupancy"] >= want, (name, r, want)
+        assert r["lds"] <= 64 * 1024, (name, r)
