@@ -43,12 +43,14 @@
 
 // Clock probe (only in the fa/libfa_hip_clock.so build, -DFA_CLOCK_PROBE=1): each workgroup of
 // the main kernels records its shader cycles and its 100 MHz real time, from which the clock the
-// kernel actually ran at follows. Compiled out of the library proper.
+// kernel actually ran at follows, plus its start on the chip-wide 100 MHz counter and where it
+// ran (HW_ID: CU, shader array and engine; XCC_ID: the chiplet), for a per-CU timeline.
+// Compiled out of the library proper.
 #ifndef FA_CLOCK_PROBE
 #define FA_CLOCK_PROBE 0
 #endif
 #if FA_CLOCK_PROBE
-__device__ unsigned long long g_fa_clock[65536][2];
+__device__ unsigned long long g_fa_clock[65536][4];
 #define FA_CLOCK_BEGIN()                                                  \
     const unsigned long long fa_c0 = __builtin_amdgcn_s_memtime();        \
     const unsigned long long fa_r0 = __builtin_amdgcn_s_memrealtime()
@@ -57,8 +59,15 @@ __device__ unsigned long long g_fa_clock[65536][2];
         const unsigned long long fa_c1 = __builtin_amdgcn_s_memtime();    \
         const unsigned long long fa_r1 = __builtin_amdgcn_s_memrealtime(); \
         if (threadIdx.x == 0 && blockIdx.x < 65536) {                     \
+            unsigned fa_hw, fa_xcc;                                       \
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n"        \
+                         "s_getreg_b32 %1, hwreg(HW_REG_XCC_ID)"           \
+                         : "=s"(fa_hw), "=s"(fa_xcc));                     \
             g_fa_clock[blockIdx.x][0] = fa_c1 - fa_c0;                    \
             g_fa_clock[blockIdx.x][1] = fa_r1 - fa_r0;                    \
+            g_fa_clock[blockIdx.x][2] = fa_r0;                            \
+            g_fa_clock[blockIdx.x][3] =                                   \
+                (static_cast<unsigned long long>(fa_xcc) << 32) | fa_hw;  \
         }                                                                 \
     } while (0)
 // Ping-pong phase timing (same build): per wave, shader cycles summed over the steady tiles
@@ -1554,8 +1563,8 @@ bool tile_of(int head_dim, bool causal, int variant, int seqlen, int64_t bh, fa_
 extern "C" {
 
 #if FA_CLOCK_PROBE
-// Copies the per-workgroup (shader cycles, 10 ns ticks) pairs of the last launch into `host`
-// (65536 x 2 entries). Exists only in the clock-probe build.
+// Copies the per-workgroup records of the last launch into `host` (65536 x 4 entries: shader
+// cycles, 10 ns ticks, start tick, XCC_ID << 32 | HW_ID). Exists only in the clock-probe build.
 int fa_probe_clock_fetch(unsigned long long* host) {
     return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fa_clock), sizeof(g_fa_clock)));
 }

@@ -1,6 +1,7 @@
 """Power and clock measurements on MI355X (not part of the attention API).
 
     PYTHONPATH=flash-attention-from-scratch_amd python3 -m fa.probe [ceiling] [clock] [busy] [phase]
+                                                                  [lds] [timeline]
 
 ceiling: TFLOPS and measured clock of pure v_mfma_f32_32x32x16_f16 streams on random fp16
          operands (8 waves per CU), alone and with the per-tile VALU work and LDS fragment reads
@@ -13,6 +14,9 @@ busy:    the same for cfg4's non-causal kernel with 16, 8, 4, 2 and 1 heads: wit
 phase:   the ping-pong kernel's steady state on cfg4, per wave group: shader cycles per tile spent
          issuing the softmax phase and the matrix phase, and waiting at each phase's end
          (s_memtime stamps at the phase-end waits of the clock-probe build).
+timeline: for the cfg4 and cfg2 kernels, the fraction of the launch's span each CU spends
+         inside a workgroup, each chiplet's finish time and clock, and the spread of workgroup
+         durations (start stamps on the chip-wide 100 MHz counter, HW_ID / XCC_ID per workgroup).
 Prints one JSON line per measurement. Build first: fa_build.py --only probe.
 """
 
@@ -75,7 +79,10 @@ def lds(blocks: int = 256, iters: int = 4000) -> None:
 def _clock_lib():
     from fa import native
 
-    so = ctypes.CDLL(str(HERE / "libfa_hip_clock.so"))
+    import os
+
+    # FA_CLOCK_LIB: another clock-probe build of the library (e.g. with -D switches) to measure
+    so = ctypes.CDLL(os.environ.get("FA_CLOCK_LIB", str(HERE / "libfa_hip_clock.so")))
     so.fa_flash_fwd.argtypes = [ctypes.POINTER(native.FaParams), ctypes.c_void_p]
     so.fa_flash_fwd.restype = ctypes.c_int
     so.fa_last_error.restype = ctypes.c_char_p
@@ -84,7 +91,7 @@ def _clock_lib():
     return so
 
 
-def _run_clock(so, q, k, v, causal: bool, reps: int = 20):
+def _run_clock(so, q, k, v, causal: bool, reps: int = 20, full: bool = False):
     import numpy as np
     import torch
 
@@ -108,13 +115,16 @@ def _run_clock(so, q, k, v, causal: bool, reps: int = 20):
         e1.record()
         e1.synchronize()
         times.append(e0.elapsed_time(e1))
-    buf = (ctypes.c_ulonglong * (65536 * 2))()
+    buf = (ctypes.c_ulonglong * (65536 * 4))()
     so.fa_probe_clock_fetch(buf)
     tile = native.tile_config(d, causal, "opt", n, b, h)
     n_wg = b * h * ((n + tile["block_q"] - 1) // tile["block_q"])
-    arr = np.frombuffer(buf, dtype=np.uint64).reshape(65536, 2)[:n_wg].astype(np.float64)
-    arr = arr[arr[:, 1] > 0]  # workgroups that recorded (e.g. not the empty split-KV ones)
+    raw = np.frombuffer(buf, dtype=np.uint64).reshape(65536, 4)[:n_wg]
+    raw = raw[raw[:, 1] > 0]  # workgroups that recorded (e.g. not the empty split-KV ones)
+    arr = raw[:, :2].astype(np.float64)
     ghz = arr[:, 0] / (arr[:, 1] * 10.0)
+    if full:
+        return statistics.median(times), raw
     return statistics.median(times), float(np.median(ghz)), float(np.median(arr[:, 0])), n_wg
 
 
@@ -180,10 +190,61 @@ def phase() -> None:
         _emit(rec)
 
 
+def timeline() -> None:
+    """Per-CU occupancy of the last launch: how much of the kernel's span each CU spent inside a
+    workgroup, when each chiplet (XCC) finished, and the spread of workgroup durations."""
+    import numpy as np
+    import torch
+
+    from fa.configs import CONFIGS, make_inputs
+
+    so = _clock_lib()
+    for name in ("cfg4", "cfg2"):
+        cfg = CONFIGS[name]
+        q, k, v = make_inputs(cfg)
+        for causal in cfg.causal:
+            ms, raw = _run_clock(so, q, k, v, causal, reps=10, full=True)
+            ticks = raw[:, 1].astype(np.int64)
+            start = raw[:, 2].astype(np.int64)
+            start = start - start.min()
+            end = start + ticks
+            span = int(end.max())
+            xcc = (raw[:, 3] >> np.uint64(32)).astype(np.int64) & 0xF
+            hw = (raw[:, 3] & np.uint64(0xFFFFFFFF)).astype(np.int64)
+            cu = xcc * 4096 + ((hw >> 8) & 0xFF)  # cu_id, sh_id, se_id (HW_ID bits 15:8)
+            ghz = raw[:, 0].astype(np.float64) / (ticks * 10.0)
+            busy_frac = []
+            for c in np.unique(cu):
+                sel = np.argsort(start[cu == c])
+                s_c, e_c = start[cu == c][sel], end[cu == c][sel]
+                covered, cur_s, cur_e = 0, s_c[0], e_c[0]
+                for a, b in zip(s_c[1:], e_c[1:]):  # union of the CU's busy intervals
+                    if a > cur_e:
+                        covered += cur_e - cur_s
+                        cur_s, cur_e = a, b
+                    else:
+                        cur_e = max(cur_e, b)
+                covered += cur_e - cur_s
+                busy_frac.append(covered / span)
+            xcc_end = [round(float(end[xcc == x].max()) / 100.0, 1) for x in np.unique(xcc)]
+            xcc_ghz = [round(float(np.median(ghz[xcc == x])), 3) for x in np.unique(xcc)]
+            _emit({"probe": "timeline", "config": name, "causal": causal, "event_ms": round(ms, 4),
+                   "span_us": round(span / 100.0, 1), "workgroups": int(len(raw)),
+                   "cus": int(len(np.unique(cu))),
+                   "cu_busy_frac_mean": round(float(np.mean(busy_frac)), 4),
+                   "cu_busy_frac_min": round(float(np.min(busy_frac)), 4),
+                   "wg_us_min_median_max": [round(float(x) / 100.0, 1) for x in
+                                            (ticks.min(), np.median(ticks), ticks.max())],
+                   "xcc_end_us": xcc_end, "xcc_clock_ghz": xcc_ghz})
+        del q, k, v
+        torch.cuda.empty_cache()
+
+
 def main(argv: list[str]) -> int:
     what = argv or ["ceiling", "clock", "busy", "phase"]
     for w in what:
-        {"ceiling": ceiling, "clock": clock, "busy": busy, "phase": phase, "lds": lds}[w]()
+        {"ceiling": ceiling, "clock": clock, "busy": busy, "phase": phase, "lds": lds,
+         "timeline": timeline}[w]()
     return 0
 
 
