@@ -8,7 +8,8 @@
 //   ldmatrix_x4_trans (common.cuh:80-84)    -> lds_read_tr16: ds_read_b64_tr_b16
 //   mma_16816 f32 acc (common.cuh:91-98)    -> mfma32: v_mfma_f32_32x32x16_f16
 //   __shfl_xor row reductions (flash_fwd.cu:359-363, 535-537)
-//                                           -> max_xor32 / sum_xor32: v_permlane32_swap
+//                                           -> max_xor32 / sum_xor32: v_permlane32_swap,
+//                                              max_xor16 / sum_xor16: v_permlane16_swap
 //   exp2f / ex2.approx (common.cuh:124-128) -> exp2_fast: v_exp_f32
 //   pack_half2 RN (common.cuh:113-117)      -> pack8: v_cvt_pk_f16_f32 (round to nearest even)
 #pragma once
@@ -84,6 +85,18 @@ __device__ __forceinline__ float max_xor32(float x) {
 }
 __device__ __forceinline__ float sum_xor32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The same with lane ^ 16 (v_permlane16_swap: the neighbouring 16-lane row).
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
                                                     false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }

@@ -57,6 +57,56 @@ constexpr int mfma32_c_col(int lane) { return lane & 31; }
 constexpr int mfma16_c_row(int lane, int r) { return 4 * (lane >> 4) + r; }
 constexpr int mfma16_c_col(int lane) { return lane & 15; }
 
+// ---- The 16x16x32 MFMA path (D = 128, 256-byte rows, 32-key tiles) --------------------------
+// Key blocks: the 16 keys of score block kb (the M rows of its MFMAs) are tile rows
+// 8kb + {0..7} and 8kb + {16..23}, i.e. row m16_key(kb, i) for M index i. A 16-lane group of a
+// K fragment read then spans both 4 KiB halves of the tile, and so does each half-wave of a
+// V^T read. Measured on MI355X (8 waves per CU, conflict-free patterns): ds_read_b128 at
+// 256 B per CU cycle with this split against 128 B with contiguous 16-row blocks (all lanes in
+// one 4 KiB half); ds_read_b64_tr_b16 at 160 B against 132 B (and 64 B for the 32x32x16 V^T
+// pattern, four lanes groups on the same four rows).
+constexpr int m16_key(int kb, int i) { return 8 * kb + (i & 7) + 16 * ((i >> 3) & 1); }
+
+// LDS swizzle of these tiles: row_xor_m16 = 2*(row%8) + (row/16)%2. K reads (16 lanes: the 16
+// rows of a key block, one logical chunk) see 16 distinct values; V^T reads (32 lanes: 8 rows,
+// 8 even or 8 odd values, logical chunks 2c and 2c+1) land on 16 distinct chunks. Rows 8
+// apart within a key block's half share the value, so the kb = 1 block and the second V^T read
+// are immediate offsets (+8 rows).
+constexpr int row_xor_m16(int row) { return ((row & 7) << 1) | ((row >> 4) & 1); }
+constexpr int swizzle_chunk_m16(int row, int chunk) { return chunk ^ row_xor_m16(row); }
+constexpr int tile_offset_m16(int row, int chunk) {
+    return row * 256 + 16 * swizzle_chunk_m16(row, chunk);
+}
+
+// K tiles of this path use their own LDS layout: the K operand of MFMA step (kb, dc) is read
+// with exactly the lane addresses of the 32x32x16 path's K fragment kk = 4kb + dc,
+// tile_offset(lane % 32, 2kk + lane / 32, 256), whose ds_read_b128 pattern measures
+// conflict-free (the direct 16x16x32 pattern, four lane groups on four chunks of the same 16
+// rows, costs 4 conflict cycles per read on MI355X). Lane l must receive key row
+// m16_key(kb, l % 16), 16-byte chunk m16_kchunk(dc, l / 16): the MFMA's k slots 8g..8g+7 of
+// lane group g are features 32g + 8dc .. +7, and the Q^T operand uses the same order.
+// m16_kslot_row / m16_kslot_chunk give the element that 16-byte LDS slot `slot` holds.
+constexpr int m16_kchunk(int dc, int grp) { return 4 * grp + dc; }
+constexpr int m16_kslot_t(int slot) { return (slot & 15) ^ row_xor(slot >> 4, 256); }
+constexpr int m16_kslot_row(int slot) {
+    return m16_key(m16_kslot_t(slot) >> 3, (slot >> 4) & 15);
+}
+constexpr int m16_kslot_chunk(int slot) {
+    return m16_kchunk((m16_kslot_t(slot) >> 1) & 3, (slot >> 8) + 2 * (m16_kslot_t(slot) & 1));
+}
+
+// S^T = K Q^T of a wave (32 queries) and a 32-key tile in four 16x16 blocks (kb, qb):
+// accumulator r of block (kb, qb) in `lane` is key st16_key(lane, kb, r) of the tile and query
+// st16_query(lane, qb) of the wave. Each lane thus holds 4 keys of 2 queries per key block.
+constexpr int st16_key(int lane, int kb, int r) { return m16_key(kb, mfma16_c_row(lane, r)); }
+constexpr int st16_query(int lane, int qb) { return 16 * qb + (lane & 15); }
+
+// Key carried by operand slot i (0..7) of the O^T += V^T P^T MFMA in `lane`: slots 0..3 are
+// the lane's scores of key block 0, slots 4..7 those of block 1, so P^T of query block qb is
+// the lane's own 8 exponentials in order (no shuffle), and the V^T operand reads these keys.
+// The key depends on lane / 16 and i only, as the MFMA's shared k index requires.
+constexpr int pv16_key(int lane, int i) { return st16_key(lane, i >> 2, i & 3); }
+
 // ---- Transposed operand reads (ds_read_b64_tr_b16) ------------------------------------------
 // Within each group of 16 lanes, the instruction loads a 4 x 16 block of 16-bit values
 // (4 rows, 16 consecutive columns) and returns it transposed: lane j of the group receives

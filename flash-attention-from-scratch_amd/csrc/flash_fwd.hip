@@ -119,8 +119,10 @@ namespace g = fa::geom;
 
 // Main-loop schedules: SIMPLE (flash_fwd_kernel), PIPE (flash_fwd_pipelined: QK of tile j+1
 // interleaved with the softmax of tile j in each wave), PINGPONG (flash_fwd_pingpong: two
-// groups of waves alternate between an MFMA-only phase and a softmax phase).
-enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3 };
+// groups of waves alternate between an MFMA-only phase and a softmax phase), KSPLIT
+// (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles), PINGPONG16
+// (flash_fwd_pingpong16: the ping-pong schedule on 16x16x32 MFMAs).
+enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3, PINGPONG16 = 4 };
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
@@ -135,7 +137,8 @@ struct Tile {
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
-    static constexpr int NBUF = SCHED == PINGPONG ? 3 : 2;  // buffers each for K and V
+    static constexpr bool M16 = SCHED == PINGPONG16;   // 16x16x32 MFMA layout and swizzle
+    static constexpr int NBUF = (SCHED == PINGPONG || M16) ? 3 : 2;  // buffers each for K, V
     static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES * KS;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
@@ -150,7 +153,8 @@ struct Tile {
 // DMA plan of one wave for a K or V tile: DMA_ITERS 16-byte-per-lane buffer->LDS copies, each
 // filling 64 consecutive physical chunk slots of the swizzled tile; the lane reads the global
 // chunk whose swizzled home is its slot. Offsets are relative to the tile's first row.
-template <class T>
+// KLAYOUT: the K-tile layout of the 16x16x32 path (fa::geom::m16_kslot_row / _chunk).
+template <class T, bool KLAYOUT = false>
 struct TileDma {
     int voff[T::DMA_ITERS];  // byte offset of the lane's source chunk
     int lds0[T::DMA_ITERS];  // wave-uniform LDS byte offset of the wave's 64 slots
@@ -159,9 +163,16 @@ struct TileDma {
         for (int it = 0; it < T::DMA_ITERS; ++it) {
             const int slot0 = (it * T::NW + wave) * 64;
             const int slot = slot0 + lane;
-            const int row = slot / T::CPR;
-            voff[it] = row * T::ROW_BYTES +
-                       16 * g::swizzle_chunk(row, slot % T::CPR, T::ROW_BYTES);
+            int row = slot / T::CPR;
+            int chunk;
+            if (KLAYOUT) {
+                row = g::m16_kslot_row(slot);
+                chunk = g::m16_kslot_chunk(slot);
+            } else {
+                chunk = T::M16 ? g::swizzle_chunk_m16(row, slot % T::CPR)
+                               : g::swizzle_chunk(row, slot % T::CPR, T::ROW_BYTES);
+            }
+            voff[it] = row * T::ROW_BYTES + 16 * chunk;
             lds0[it] = slot0 * 16;
         }
     }
@@ -171,9 +182,9 @@ struct TileDma {
 // covers rows [kt, n) only, so rows >= n are zero-filled by the hardware range check (their
 // scores are masked, and zero V rows keep 0 * garbage from ever forming a NaN); the per-tile
 // offset lives in the scalar resource, so a refill costs no VALU work.
-template <class T>
+template <class T, bool KL = false>
 __device__ __forceinline__ void load_tile(const f16* head, int kt, int n, char* lds,
-                                          const TileDma<T>& dma) {
+                                          const TileDma<T, KL>& dma) {
     const char* base = reinterpret_cast<const char*>(head) + static_cast<size_t>(kt) * T::ROW_BYTES;
     const auto rsrc = make_rsrc(base, static_cast<unsigned>(max(0, n - kt)) * T::ROW_BYTES);
 #pragma unroll
@@ -1249,6 +1260,465 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     FA_CLOCK_END();
 }
 
+// ---- ping-pong on 16x16x32 MFMAs (D = 128) ----------------------------------------------------
+// The schedule and buffer protocol of flash_fwd_pingpong, with the matrix work on
+// v_mfma_f32_16x16x32_f16 (two of half the FLOPs per 32x32x16). On MI355X, which runs this
+// kernel at its power limit, a stream of 16x16x32 MFMAs on random fp16 data sustains about
+// 20 % more FLOPS than the same FLOPs in 32x32x16 MFMAs: the chip holds a higher clock.
+// Per wave (32 queries) and 32-key tile: S^T in four 16x16 blocks s[kb][qb] (keys 16kb..,
+// queries 16qb..), so a lane holds 4 keys of each of two queries (lane % 16 and 16 + lane % 16)
+// and keeps a running max and sum per query block. P^T of query block qb is the lane's own
+// 8 exponentials, in the key order fa::geom::pv16_key that the V^T operand reads. O^T in 16
+// blocks oacc[db][qb] (features 16db.., queries 16qb..). The LDS tiles use the swizzle
+// fa::geom::row_xor_m16, conflict-free for these read patterns.
+namespace m16 {
+constexpr int KB = 2;  // 16-key blocks per 32-key tile
+constexpr int QB = 2;  // 16-query blocks per wave
+constexpr int DC = 4;  // 32-deep MFMA steps over D = 128
+constexpr int DB = 8;  // 16-wide feature blocks over D = 128
+constexpr int ROW = 256;  // bytes per K/V row
+}  // namespace m16
+
+// Lane-dependent LDS offsets: K fragment (kb, dc) at the 32x32x16 path's fragment address for
+// kk = 4kb + dc (the K tile's own layout, fa::geom::m16_kslot_row); V^T fragment db: the 4 rows
+// pv16_key(lane, 0..3) (via the tr16 addressing of a 4-row block), 16 feature columns from
+// 16db (the second read, keys pv16_key(lane, 4..7), is 8 rows further).
+struct Frag16 {
+    int koff[m16::KB][m16::DC];
+    int voff[m16::DB];
+    __device__ __forceinline__ explicit Frag16(int lane) {
+#pragma unroll
+        for (int kb = 0; kb < m16::KB; ++kb)
+#pragma unroll
+            for (int dc = 0; dc < m16::DC; ++dc)
+                koff[kb][dc] = g::tile_offset(lane & 31, 2 * (4 * kb + dc) + (lane >> 5), m16::ROW);
+#pragma unroll
+        for (int db = 0; db < m16::DB; ++db) {
+            const int row = g::pv16_key(lane, 0) + g::tr16_row(lane);
+            const int c = 16 * db + g::tr16_col(lane);  // halves
+            voff[db] = g::tile_offset_m16(row, c >> 3) + 2 * (c & 7);
+        }
+    }
+};
+
+// Q^T operands: qf[qb][dc] holds Q[qw + 16qb + lane%16][8 * m16_kchunk(dc, lane/16) .. +7],
+// the feature order of the K operand.
+__device__ __forceinline__ void load_q16(const f16* qh, int qw, int n, int lane, int negate_q,
+                                         f16x8 (&qf)[m16::QB][m16::DC]) {
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb) {
+        const int row = min(qw + 16 * qb + (lane & 15), n - 1);
+        const f16* src = qh + static_cast<size_t>(row) * 128;
+#pragma unroll
+        for (int dc = 0; dc < m16::DC; ++dc) {
+            qf[qb][dc] = *reinterpret_cast<const f16x8*>(src + 8 * g::m16_kchunk(dc, lane >> 4));
+            if (negate_q) qf[qb][dc] = -qf[qb][dc];
+        }
+    }
+}
+
+// K fragments of a tile (8 ds_read_b128) and V^T fragments (16 ds_read_b64_tr_b16).
+__device__ __forceinline__ void load_k16(const char* kl, const Frag16& fr,
+                                         f16x8 (&kf)[m16::KB][m16::DC]) {
+#pragma unroll
+    for (int kb = 0; kb < m16::KB; ++kb)
+#pragma unroll
+        for (int dc = 0; dc < m16::DC; ++dc)
+            kf[kb][dc] = *reinterpret_cast<const f16x8*>(kl + fr.koff[kb][dc]);
+}
+__device__ __forceinline__ void load_v16(const char* vl, const Frag16& fr,
+                                         f16x8 (&vf)[m16::DB]) {
+#pragma unroll
+    for (int db = 0; db < m16::DB; ++db) {
+        const f16x4 lo = lds_read_tr16(vl + fr.voff[db]);
+        const f16x4 up = lds_read_tr16(vl + fr.voff[db] + 8 * m16::ROW);
+        vf[db] = f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+    }
+}
+
+// S^T = K Q^T of one tile (the first one, before the steady phases).
+__device__ __forceinline__ void qk16(const char* kl, const Frag16& fr,
+                                     const f16x8 (&qf)[m16::QB][m16::DC],
+                                     f32x4 (&s)[m16::KB][m16::QB]) {
+    f16x8 kf[m16::KB][m16::DC];
+    load_k16(kl, fr, kf);
+#pragma unroll
+    for (int kb = 0; kb < m16::KB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < m16::QB; ++qb) {
+            s[kb][qb] = f32x4{};
+#pragma unroll
+            for (int dc = 0; dc < m16::DC; ++dc) s[kb][qb] = mfma16(kf[kb][dc], qf[qb][dc], s[kb][qb]);
+        }
+}
+
+// Keys >= n, and (causal) keys right of the query, get -inf.
+template <bool CAUSAL>
+__device__ __forceinline__ void mask16(f32x4 (&s)[m16::KB][m16::QB], int kt, int n, int qw,
+                                       int lane) {
+#pragma unroll
+    for (int kb = 0; kb < m16::KB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < m16::QB; ++qb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kt + g::st16_key(lane, kb, r);
+                const int query = qw + g::st16_query(lane, qb);
+                const bool masked = key >= n || (CAUSAL && key > query);
+                s[kb][qb][r] = masked ? -INFINITY : s[kb][qb][r];
+            }
+}
+
+// Optimistic softmax against the running max (as softmax_optimistic): P in fp16 and l += row
+// sums, unless some p overflowed fp16, in which case `overflow` is set (wave-uniform) and the
+// caller redoes the tile exactly.
+__device__ __forceinline__ void softmax16_optimistic(const f32x4 (&s)[m16::KB][m16::QB],
+                                                     float scale_log2,
+                                                     const float (&m_run)[m16::QB],
+                                                     float (&l_run)[m16::QB], bool& overflow,
+                                                     f16x8 (&p)[m16::QB]) {
+    // All 16 exponentials first, then the packs and the two row sums: a pack or sum right after
+    // the exponentials it reads would wait on their latency.
+    float e[m16::QB][8];
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            e[qb][i] = exp2_fast(fmaf(s[i >> 2][qb][i & 3], scale_log2, -m_run[qb]));
+    float sum[m16::QB] = {0.0F, 0.0F};
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb)
+        p[qb] = pack8(e[qb][0], e[qb][1], e[qb][2], e[qb][3], e[qb][4], e[qb][5], e[qb][6],
+                      e[qb][7]);
+    // The two sums as interleaved v_dot2 chains.
+    const f16x2 one = {static_cast<f16>(1.0F), static_cast<f16>(1.0F)};
+#define FA_SUM2(K)                                                                              \
+    for (int qb = 0; qb < m16::QB; ++qb)                                                       \
+        sum[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(p[qb], p[qb], 2 * (K),        \
+                                                                 2 * (K) + 1),                  \
+                                         one, sum[qb], false);
+    FA_SUM2(0)
+    FA_SUM2(1)
+    FA_SUM2(2)
+    FA_SUM2(3)
+#undef FA_SUM2
+    overflow = wave_any(!(sum[0] < INFINITY && sum[1] < INFINITY));
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb) l_run[qb] = overflow ? l_run[qb] : l_run[qb] + sum[qb];
+}
+
+// Exact online softmax of one tile (as softmax_tile): the tile max of a query spans the four
+// lanes lane % 16 + 16*i that hold its keys.
+template <class T>
+__device__ __forceinline__ void softmax16_tile(const f32x4 (&s)[m16::KB][m16::QB],
+                                               float scale_log2, float (&m_run)[m16::QB],
+                                               float (&l_run)[m16::QB], float (&alpha)[m16::QB],
+                                               bool& rescale, f16x8 (&p)[m16::QB]) {
+    float mx[m16::QB];
+    bool grow = false;
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb) {
+        float x = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x = fmaxf(x, s[i >> 2][qb][i & 3]);
+        mx[qb] = max_xor32(max_xor16(x)) * scale_log2;
+        grow = grow || (T::LAZY ? (mx[qb] > m_run[qb] + 8.0F) : (mx[qb] > m_run[qb]));
+    }
+    rescale = wave_any(grow);
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb) {
+        const float m_new = rescale ? fmaxf(m_run[qb], mx[qb]) : m_run[qb];
+        const float m_use = (m_new == -INFINITY) ? 0.0F : m_new;
+        alpha[qb] = exp2_fast(m_run[qb] - m_use);
+        m_run[qb] = m_new;
+        float e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = exp2_fast(fmaf(s[i >> 2][qb][i & 3], scale_log2, -m_use));
+        p[qb] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+        l_run[qb] = (rescale ? l_run[qb] * alpha[qb] : l_run[qb]) + sum8_f16(p[qb], 0.0F);
+    }
+}
+
+__device__ __forceinline__ void rescale16(f32x4 (&oacc)[m16::DB][m16::QB],
+                                          const float (&alpha)[m16::QB]) {
+#pragma unroll
+    for (int db = 0; db < m16::DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < m16::QB; ++qb) oacc[db][qb] *= alpha[qb];
+}
+
+__device__ __forceinline__ void pv16(const f16x8 (&vf)[m16::DB], const f16x8 (&p)[m16::QB],
+                                     f32x4 (&oacc)[m16::DB][m16::QB]) {
+#pragma unroll
+    for (int db = 0; db < m16::DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < m16::QB; ++qb) oacc[db][qb] = mfma16(vf[db], p[qb], oacc[db][qb]);
+}
+
+// Matrix phase: S^T_{j+1} (16 MFMAs, four independent chains of 4) alternating with
+// O^T += V_j^T P_j^T (16 MFMAs, independent); `mid` (the refill) after the first 8.
+template <class Mid>
+__device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[m16::KB][m16::DC],
+                                               const f16x8 (&qf)[m16::QB][m16::DC],
+                                               const f16x8 (&vf)[m16::DB],
+                                               const f16x8 (&p)[m16::QB],
+                                               f32x4 (&s)[m16::KB][m16::QB],
+                                               f32x4 (&oacc)[m16::DB][m16::QB], Mid&& mid) {
+#pragma unroll
+    for (int kb = 0; kb < m16::KB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < m16::QB; ++qb) s[kb][qb] = f32x4{};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int kb = (i >> 1) & 1;
+        const int qs = i & 1;
+        const int dc = i >> 2;
+        s[kb][qs] = mfma16(kf[kb][dc], qf[qs][dc], s[kb][qs]);
+        const int db = i >> 1;
+        oacc[db][qs] = mfma16(vf[db], p[qs], oacc[db][qs]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the alternation
+        if (i == 3) {
+            mid();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// O = acc / l as fp16 for the lane's two queries (if < n), and the natural-log LSE if lse_h is
+// not null. The lane holds features 16db + 4*(lane/16) + 0..3: one 8-byte store per db.
+__device__ __forceinline__ void store16(f16* oh, float* lse_h, int qw, int n, int lane,
+                                        const float (&m_run)[m16::QB],
+                                        const float (&l_run)[m16::QB],
+                                        const f32x4 (&oacc)[m16::DB][m16::QB]) {
+    float l_tot[m16::QB];
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb) l_tot[qb] = sum_xor32(sum_xor16(l_run[qb]));
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb) {
+        const int qrow = qw + g::st16_query(lane, qb);
+        if (qrow >= n) continue;
+        const float inv = (l_tot[qb] > 0.0F) ? (1.0F / l_tot[qb]) : 0.0F;
+        if (lse_h != nullptr && lane < 16) lse_h[qrow] = row_lse2(m_run[qb], l_tot[qb]) * kLn2;
+        f16* dst = oh + static_cast<size_t>(qrow) * 128 + 4 * (lane >> 4);
+#pragma unroll
+        for (int db = 0; db < m16::DB; ++db) {
+            const f32x4& a = oacc[db][qb];
+            *reinterpret_cast<f16x4*>(dst + 16 * db) =
+                pack4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+        }
+    }
+}
+
+// Tiles j .. n_tiles-1 outside the steady phases (as general_tiles): one barrier each; K_t
+// and V_t in buffer t % 3; refills of K_{j+2} and V_{j+1}.
+template <class T, bool CAUSAL>
+__device__ __forceinline__ void general_tiles16(
+    int j, int n_tiles, int n_act, int n, int qw, int lane, const f16* kh, const f16* vh,
+    char* const (&kb)[3], char* const (&vb)[3], const TileDma<T, true>& dma_k,
+    const TileDma<T>& dma, const Frag16& fr,
+    const f16x8 (&qf)[m16::QB][m16::DC], f32x4 (&s)[m16::KB][m16::QB],
+    f32x4 (&oacc)[m16::DB][m16::QB], float scale_log2, float (&m_run)[m16::QB],
+    float (&l_run)[m16::QB]) {
+    for (; j < n_tiles; ++j) {
+        wait_vmem();
+        __syncthreads();
+        const bool act = j < n_act;
+        const bool act_next = j + 1 < n_act;
+        f16x8 kf[m16::KB][m16::DC];
+        f16x8 vf[m16::DB];
+        if (act_next) load_k16(kb[(j + 1) % 3], fr, kf);
+        if (act) load_v16(vb[j % 3], fr, vf);
+        if (j + 2 < n_tiles) load_tile<T>(kh, (j + 2) * T::BC, n, kb[(j + 2) % 3], dma_k);
+        if (j + 1 < n_tiles) load_tile<T>(vh, (j + 1) * T::BC, n, vb[(j + 1) % 3], dma);
+        if (!act) continue;  // wave-uniform: fully masked for this wave (causal)
+        f32x4 s2[m16::KB][m16::QB];
+        if (act_next) {
+#pragma unroll
+            for (int b = 0; b < m16::KB; ++b)
+#pragma unroll
+                for (int qb = 0; qb < m16::QB; ++qb) {
+                    s2[b][qb] = f32x4{};
+#pragma unroll
+                    for (int dc = 0; dc < m16::DC; ++dc)
+                        s2[b][qb] = mfma16(kf[b][dc], qf[qb][dc], s2[b][qb]);
+                }
+        }
+        const int kt = j * T::BC;
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask16<CAUSAL>(s, kt, n, qw, lane);
+        f16x8 p[m16::QB];
+        float alpha[m16::QB];
+        bool rescale;
+        softmax16_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale16(oacc, alpha);
+        pv16(vf, p, oacc);
+        if (act_next) {
+#pragma unroll
+            for (int b = 0; b < m16::KB; ++b)
+#pragma unroll
+                for (int qb = 0; qb < m16::QB; ++qb) s[b][qb] = s2[b][qb];
+        }
+    }
+}
+
+template <class T, bool CAUSAL>
+__global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
+    float* /*lse_part*/) {
+    static_assert(T::D == 128 && T::BC == 32, "the 16x16x32 layout is written for D=128, BC=32");
+    static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
+    static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
+    static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
+    FA_CLOCK_BEGIN();
+    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds2[T::TILE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_uniform(threadIdx.x >> 6);
+    const int grp = wave >> 2;
+    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
+    const f16* kh = k + head;
+    const f16* vh = v + head;
+    const int q0 = w.qb * T::BR;
+    const int qw = q0 + wave * 32;
+    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
+    // Every tile but the last runs in the steady phases (diagonal and tail tiles masked there).
+    const int n_steady = max(0, n_tiles - 1);
+
+    auto kbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? k_lds0 : (B == 1 ? k_lds1 : k_lds2);
+    };
+    auto vbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? v_lds0 : (B == 1 ? v_lds1 : v_lds2);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+
+    const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
+    const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
+    load_tile<T>(kh, 0, n, kbuf(I0{}), dma_k);
+    load_tile<T>(vh, 0, n, vbuf(I0{}), dma);
+    load_tile<T>(kh, T::BC, n, kbuf(I1{}), dma_k);
+    load_tile<T>(kh, 2 * T::BC, n, kbuf(I2{}), dma_k);
+    load_tile<T>(vh, T::BC, n, vbuf(I1{}), dma);
+    f16x8 qf[m16::QB][m16::DC];
+    load_q16(q + head, qw, n, lane, negate_q, qf);
+    const Frag16 fr(lane);
+
+    f32x4 oacc[m16::DB][m16::QB];
+#pragma unroll
+    for (int db = 0; db < m16::DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < m16::QB; ++qb) oacc[db][qb] = f32x4{};
+    float m_run[m16::QB] = {-INFINITY, -INFINITY};
+    float l_run[m16::QB] = {0.0F, 0.0F};
+
+    wait_vmem();
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < m16::QB; ++qb)
+#pragma unroll
+        for (int dc = 0; dc < m16::DC; ++dc) asm volatile("" ::"v"(qf[qb][dc]));
+    f32x4 s[m16::KB][m16::QB];
+    if (n_act > 0) qk16(kbuf(I0{}), fr, qf, s);
+
+    FA_PHASE_DECL();
+    auto steady = [&](auto group) {
+        constexpr int G = decltype(group)::value;
+        auto refill = [&](int a, auto pa, int b, auto pb) {
+            load_tile<T>(kh, a * T::BC, n, kbuf(pa), dma_k);
+            load_tile<T>(vh, b * T::BC, n, vbuf(pb), dma);
+        };
+        end_phase<false>();
+        if constexpr (G == 1) {
+            refill(3, I0{}, 2, I2{});
+            end_phase<false>();
+        }
+        auto tile = [&](int jj, auto r) {
+            FA_PHASE_T(ta);
+            constexpr int R = decltype(r)::value;
+            using Rj = std::integral_constant<int, R>;
+            using Rj1 = std::integral_constant<int, (R + 1) % 3>;
+            using Rj2 = std::integral_constant<int, (R + 2) % 3>;
+            // softmax phase S_jj
+            if (g::tile_needs_mask(n, jj * T::BC, T::BC, qw, CAUSAL)) {
+                mask16<CAUSAL>(s, jj * T::BC, n, qw, lane);
+            }
+            f16x8 kf[m16::KB][m16::DC];
+            f16x8 vf[m16::DB];
+            load_k16(kbuf(Rj1{}), fr, kf);
+            load_v16(vbuf(Rj{}), fr, vf);
+            f16x8 p[m16::QB];
+            bool overflow;
+            softmax16_optimistic(s, scale_log2, m_run, l_run, overflow, p);
+            sched_reads_valu<FA_PP_READS_PER, FA_PP_VALU_PER, 24 / FA_PP_READS_PER>();
+            FA_PHASE_T(tb);
+            end_phase<G == 1>();
+            FA_PHASE_T(tc);
+            // matrix phase M_jj
+            if (__builtin_expect(overflow, 0)) {
+                float alpha[m16::QB];
+                bool rescale;
+                softmax16_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+                if (rescale) rescale16(oacc, alpha);
+            }
+            __builtin_amdgcn_s_setprio(FA_PP_PRIO);
+            matrix_phase16(kf, qf, vf, p, s, oacc, [&] {
+                if constexpr (G == 0) {
+                    refill(jj + 3, Rj{}, jj + 2, Rj2{});
+                } else {
+                    refill(jj + 4, Rj1{}, jj + 3, Rj{});
+                }
+            });
+            __builtin_amdgcn_s_setprio(0);
+            FA_PHASE_T(td);
+            end_phase<G == 0>();
+            FA_PHASE_T(te);
+            FA_PHASE_TILE(ta, tb, tc, td, te);
+        };
+        int jj = 0;
+        for (; jj + 3 <= n_steady; jj += 3) {
+            tile(jj, I0{});
+            tile(jj + 1, I1{});
+            tile(jj + 2, I2{});
+        }
+        if (jj < n_steady) tile(jj, I0{});
+        if (jj + 1 < n_steady) tile(jj + 1, I1{});
+        if constexpr (G == 0) end_phase<false>();
+    };
+    if (n_steady > 0) {
+        if (grp == 0) {
+            steady(I0{});
+        } else {
+            steady(I1{});
+        }
+    }
+    char* kb[3];
+    char* vb[3];
+    kb[0] = k_lds0;
+    kb[1] = k_lds1;
+    kb[2] = k_lds2;
+    vb[0] = v_lds0;
+    vb[1] = v_lds1;
+    vb[2] = v_lds2;
+    general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, n, qw, lane, kh, vh, kb, vb, dma_k, dma,
+                               fr, qf, s, oacc, scale_log2, m_run, l_run);
+    store16(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane, m_run,
+            l_run, oacc);
+    FA_PHASE_STORE(wave, lane);
+    FA_CLOCK_END();
+}
+
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
 // (csrc/kernels/flash_fwd.cu:597-612). On MI355X the best tile also depends on the sequence
@@ -1290,13 +1760,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 #define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG
 #endif
 #ifndef FA_OPT_D128
-#define FA_OPT_D128 32, 8, true, PINGPONG
+#define FA_OPT_D128 32, 8, true, PINGPONG16
 #endif
 #ifndef FA_OPT_D128_CAUSAL_SHORT
 #define FA_OPT_D128_CAUSAL_SHORT 32, 4, true, SIMPLE
 #endif
 #ifndef FA_OPT_D128_CAUSAL
-#define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG
+#define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG16
 #endif
 #ifndef FA_D64_SHORT_MAX_N
 #define FA_D64_SHORT_MAX_N 2048
@@ -1441,6 +1911,8 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
         fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
     } else if constexpr (T::SCHED == PINGPONG) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
+    } else if constexpr (T::SCHED == PINGPONG16) {
+        fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL>);
     } else if constexpr (T::SCHED == KSPLIT) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
     } else if constexpr (T::SCHED == PIPE) {

@@ -5,7 +5,8 @@
 
 ceiling: TFLOPS and measured clock of pure v_mfma_f32_32x32x16_f16 streams on random fp16
          operands (8 waves per CU), alone and with the per-tile VALU work and LDS fragment reads
-         of attention added (fa/libfa_probe.so, csrc/fa_probe.hip).
+         of attention added, and of a v_mfma_f32_16x16x32_f16 stream of the same FLOPs
+         (fa/libfa_probe.so, csrc/fa_probe.hip).
 clock:   the clock the attention kernels themselves run at, and their shader cycles per
          workgroup, on the benchmark shapes (fa/libfa_hip_clock.so: the library built with
          per-workgroup s_memtime / s_memrealtime recording).
@@ -40,21 +41,24 @@ def _emit(rec: dict) -> None:
 def ceiling(blocks: int = 1024, iters: int = 2000) -> None:
     so = ctypes.CDLL(str(HERE / "libfa_probe.so"))
     so.fa_probe_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int,
                                     ctypes.POINTER(ctypes.c_float),
                                     ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double)]
-    for valu, lds in ((0, 0), (1, 0), (0, 1), (1, 1)):
+    for shape, valu, lds in ((s, v, l) for s in (0, 1) for v, l in ((0, 0), (1, 0), (0, 1), (1, 1))):
         ms, ghz, cyc = ctypes.c_float(), ctypes.c_double(), ctypes.c_double()
-        rc = so.fa_probe_ceiling(valu, lds, blocks, iters, ctypes.byref(ms), ctypes.byref(ghz),
-                                 ctypes.byref(cyc))
+        rc = so.fa_probe_ceiling(valu, lds, shape, blocks, iters, ctypes.byref(ms),
+                                 ctypes.byref(ghz), ctypes.byref(cyc))
         if rc != 0:
             raise RuntimeError(f"fa_probe_ceiling failed with HIP status {rc}")
         flops = blocks * 8 * iters * 16 * 32768.0
         tf = flops / (ms.value * 1e-3) / 1e12
-        _emit({"probe": "mfma_ceiling", "softmax_valu": bool(valu), "lds_fragments": bool(lds),
+        _emit({"probe": "mfma_ceiling",
+               "mfma": "16x16x32" if shape else "32x32x16",
+               "softmax_valu": bool(valu), "lds_fragments": bool(lds),
                "tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
                "clock_ghz": round(ghz.value, 3),
-               "cycles_per_16_mfma_per_simd": round(cyc.value / iters, 1)})
+               "cycles_per_iteration_per_workgroup": round(cyc.value / iters, 1)})
 
 
 def lds(blocks: int = 256, iters: int = 4000) -> None:
@@ -63,7 +67,13 @@ def lds(blocks: int = 256, iters: int = 4000) -> None:
     so.fa_probe_lds.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_double),
                                 ctypes.POINTER(ctypes.c_double)]
-    for mode, name, bytes_per_read in ((0, "ds_read_b128", 16), (1, "ds_read_b64_tr_b16", 8)):
+    for mode, name, bytes_per_read in ((0, "ds_read_b128", 16), (1, "ds_read_b64_tr_b16", 8),
+                                       (2, "ds_read_b128 (16x16x32 K)", 16),
+                                       (3, "ds_read_b64_tr_b16 (16x16x32 V^T)", 8),
+                                       (4, "ds_read_b64_tr_b16 (16x16x32 V^T, unswizzled)", 8),
+                                       (5, "ds_read_b128 (16x16x32 K, split key blocks)", 16),
+                                       (6, "ds_read_b64_tr_b16 (16x16x32 V^T, split key blocks)",
+                                        8)):
         ms, ghz, cyc = ctypes.c_float(), ctypes.c_double(), ctypes.c_double()
         rc = so.fa_probe_lds(mode, blocks, iters, ctypes.byref(ms), ctypes.byref(ghz),
                              ctypes.byref(cyc))

@@ -84,6 +84,12 @@ __global__ void k_xor32(const float* in, float* out_max, float* out_sum) {
     out_sum[l] = sum_xor32(in[l]);
 }
 
+__global__ void k_xor16(const float* in, float* out_max, float* out_sum) {
+    const int l = threadIdx.x;
+    out_max[l] = max_xor16(in[l]);
+    out_sum[l] = sum_xor16(in[l]);
+}
+
 __global__ void k_exp2(const float* x, float* y, int n) {
     for (int i = threadIdx.x; i < n; i += 64) y[i] = exp2_fast(x[i]);
 }
@@ -213,6 +219,18 @@ int fab_xor32(const float* in, float* out_max, float* out_sum) {
     FAB_TRY(dm.err);
     FAB_TRY(ds.err);
     hipLaunchKernelGGL(k_xor32, dim3(1), dim3(64), 0, 0, di.p, dm.p, ds.p);
+    FAB_TRY(hipGetLastError());
+    FAB_TRY(hipDeviceSynchronize());
+    FAB_TRY(to_host(out_max, dm, 64));
+    return to_host(out_sum, ds, 64);
+}
+
+int fab_xor16(const float* in, float* out_max, float* out_sum) {
+    DevBuf<float> di(64), dm(64), ds(64);
+    FAB_TRY(to_dev(di, in, 64));
+    FAB_TRY(dm.err);
+    FAB_TRY(ds.err);
+    hipLaunchKernelGGL(k_xor16, dim3(1), dim3(64), 0, 0, di.p, dm.p, ds.p);
     FAB_TRY(hipGetLastError());
     FAB_TRY(hipDeviceSynchronize());
     FAB_TRY(to_host(out_max, dm, 64));

@@ -70,12 +70,15 @@ def test_mfma_layout_exact(blk, shape):
     np.testing.assert_array_equal(c, a.astype(np.float32) @ b.astype(np.float32))
 
 
-def test_permlane32_pair_reductions(blk):
+@pytest.mark.parametrize("dist", [32, 16])
+def test_permlane_pair_reductions(blk, dist):
+    """max/sum with lane ^ 32 (v_permlane32_swap) and lane ^ 16 (v_permlane16_swap)."""
     x = np.random.default_rng(4).standard_normal(64).astype(np.float32)
     mx = np.zeros(64, np.float32)
     sm = np.zeros(64, np.float32)
-    _ok(blk.fab_xor32(_ptr(x), _ptr(mx), _ptr(sm)))
-    partner = x[np.arange(64) ^ 32]
+    fn = blk.fab_xor32 if dist == 32 else blk.fab_xor16
+    _ok(fn(_ptr(x), _ptr(mx), _ptr(sm)))
+    partner = x[np.arange(64) ^ dist]
     np.testing.assert_array_equal(mx, np.maximum(x, partner))
     np.testing.assert_array_equal(sm, x + partner)
 

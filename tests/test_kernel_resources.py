@@ -19,7 +19,7 @@ import pytest
 RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" / "fa" / \
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
-SIMPLE, PIPE, PINGPONG, KSPLIT = 0, 1, 2, 3
+SIMPLE, PIPE, PINGPONG, KSPLIT, PINGPONG16 = 0, 1, 2, 3, 4
 
 
 def _load():
@@ -32,7 +32,7 @@ def _min_occupancy(name: str) -> int:
     if "flash_fwd_combine" in name:
         return 4
     d, bc, nw, _lazy, sched = (int(x) for x in TILE.search(name).groups())
-    if "flash_fwd_pingpong" in name:
+    if "flash_fwd_pingpong" in name:  # flash_fwd_pingpong and flash_fwd_pingpong16
         return 2                      # waves w and w+4 share a SIMD
     if "flash_fwd_ksplit" in name:
         return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
