@@ -1271,6 +1271,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 // 8 exponentials, in the key order fa::geom::pv16_key that the V^T operand reads. O^T in 16
 // blocks oacc[db][qb] (features 16db.., queries 16qb..). The LDS tiles use the swizzle
 // fa::geom::row_xor_m16, conflict-free for these read patterns.
+// Fragment reads and softmax VALU of the softmax phase: N times {R reads, V VALU} (as
+// FA_PP_READS_PER / FA_PP_VALU_PER for flash_fwd_pingpong); R must divide the 24 reads.
+#ifndef FA_PP16_READS_PER
+#define FA_PP16_READS_PER 8
+#endif
+#ifndef FA_PP16_VALU_PER
+#define FA_PP16_VALU_PER 16
+#endif
 namespace m16 {
 constexpr int KB = 2;  // 16-key blocks per 32-key tile
 constexpr int QB = 2;  // 16-query blocks per wave
@@ -1661,7 +1669,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             f16x8 p[m16::QB];
             bool overflow;
             softmax16_optimistic(s, scale_log2, m_run, l_run, overflow, p);
-            sched_reads_valu<FA_PP_READS_PER, FA_PP_VALU_PER, 24 / FA_PP_READS_PER>();
+            static_assert(24 % FA_PP16_READS_PER == 0, "FA_PP16_READS_PER must divide 24");
+            sched_reads_valu<FA_PP16_READS_PER, FA_PP16_VALU_PER, 24 / FA_PP16_READS_PER>();
             FA_PHASE_T(tb);
             end_phase<G == 1>();
             FA_PHASE_T(tc);
