@@ -5,8 +5,9 @@
 Averages every counter over the attention kernel's dispatches except the first (the driver's
 checked launch, which runs on a cold cache and clock), and derives:
   * MFMA utilisation: SQ_VALU_MFMA_BUSY_CYCLES per SIMD over GRBM_GUI_ACTIVE per XCD;
-  * matrix FLOPs from SQ_INSTS_MFMA (32768 FLOPs per v_mfma_f32_32x32x16_f16) against the
-    algorithmic 4*B*H*N^2*d (halved for causal): a ratio above 1 is wasted matrix work;
+  * matrix FLOPs from SQ_INSTS_MFMA (32768 FLOPs per v_mfma_f32_32x32x16_f16, 16384 per
+    v_mfma_f32_16x16x32_f16 in flash_fwd_pingpong16) against the algorithmic 4*B*H*N^2*d
+    (halved for causal): a ratio above 1 is wasted matrix work;
   * LDS bank-conflict rate, MFMA/VALU co-execution, waits on LDS;
   * HBM bytes = FETCH_SIZE * fetch_scale + WRITE_SIZE * write_scale (KiB), against the
     algorithmic 4*B*H*N*d*2 bytes (Q, K, V read once, O written once). The scales convert the
@@ -24,7 +25,9 @@ import sys
 from collections import defaultdict
 from pathlib import Path
 
-FLOPS_PER_MFMA = 2 * 32 * 32 * 16
+def flops_per_mfma(kernel_name: str) -> int:
+    """flash_fwd_pingpong16 issues v_mfma_f32_16x16x32_f16; the other kernels 32x32x16."""
+    return 2 * 16 * 16 * 32 if "pingpong16" in kernel_name else 2 * 32 * 32 * 16
 
 
 def _counters(path: Path, kernel: str) -> dict[str, float]:
@@ -89,18 +92,20 @@ def main(argv: list[str]) -> int:
         row("average duration", f"{avg * 1e3:.4f} ms (min {min(durs) * 1e3:.4f})")
         row("TFLOPS (algorithmic / average)",
             f"{flops / avg / 1e12:.1f} ({100 * flops / avg / 1e12 / a.peak_tflops:.1f} % of peak)")
+    fpm = flops_per_mfma(name)
+    shape = "16x16x32" if fpm == 16384 else "32x32x16"
     if "SQ_INSTS_MFMA" in c:
-        row("MFMA FLOPs / algorithmic FLOPs", f"{c['SQ_INSTS_MFMA'] * FLOPS_PER_MFMA / flops:.4f}")
+        row("MFMA FLOPs / algorithmic FLOPs", f"{c['SQ_INSTS_MFMA'] * fpm / flops:.4f}")
     if "SQ_VALU_MFMA_BUSY_CYCLES" in c and "GRBM_GUI_ACTIVE" in c:
         busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / a.simds
         active = c["GRBM_GUI_ACTIVE"] / a.xcds
         row("MFMA busy per SIMD / GPU active cycles", f"{busy:,.0f} / {active:,.0f} = "
             f"{100 * busy / active:.1f} %")
     if "SQ_INSTS_VALU" in c and "SQ_INSTS_MFMA" in c:
-        row("non-MFMA VALU instructions per MFMA",
+        row(f"non-MFMA VALU instructions per MFMA ({shape})",
             f"{(c['SQ_INSTS_VALU'] - c['SQ_INSTS_MFMA']) / c['SQ_INSTS_MFMA']:.2f}")
     if "SQ_INSTS_VALU_TRANS_F32" in c and "SQ_INSTS_MFMA" in c:
-        row("transcendental (v_exp_f32 ...) per MFMA",
+        row(f"transcendental (v_exp_f32 ...) per MFMA ({shape})",
             f"{c['SQ_INSTS_VALU_TRANS_F32'] / c['SQ_INSTS_MFMA']:.2f}")
     if "SQ_LDS_BANK_CONFLICT" in c and "SQ_LDS_IDX_ACTIVE" in c and c["SQ_LDS_IDX_ACTIVE"]:
         row("LDS bank-conflict cycles / LDS active cycles",
