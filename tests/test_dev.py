@@ -48,15 +48,17 @@ def _write_csv(path: Path, header: list[str], rows: list[list]):
         w.writerows(rows)
 
 
-def test_counters_summary(tmp_path):
+@pytest.mark.parametrize("kname, fpm, shape", [("_ZN2fa18flash_fwd_pingpongE", 32768, "32x32x16"),
+                                               ("_ZN2fa20flash_fwd_pingpong16E", 16384, "16x16x32")])
+def test_counters_summary(tmp_path, kname, fpm, shape):
     """Two dispatches of a kernel: the first (the checked launch) is dropped, and the derived
-    figures follow from the second one's counters."""
-    kname = "_ZN2fa18flash_fwd_pingpongE"
+    figures follow from the second one's counters; MFMA FLOPs per instruction follow the
+    kernel (flash_fwd_pingpong16 issues 16x16x32 MFMAs)."""
     b, h, n, d = 1, 2, 1024, 128
     flops = 4.0 * b * h * n * n * d
     hdr = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
-    second = {"SQ_INSTS_MFMA": flops / 32768, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 500.0,
-              "GRBM_GUI_ACTIVE": 8 * 1000.0, "SQ_INSTS_VALU": 4 * flops / 32768,
+    second = {"SQ_INSTS_MFMA": flops / fpm, "SQ_VALU_MFMA_BUSY_CYCLES": 1024 * 500.0,
+              "GRBM_GUI_ACTIVE": 8 * 1000.0, "SQ_INSTS_VALU": 4 * flops / fpm,
               "SQ_LDS_BANK_CONFLICT": 0.0, "SQ_LDS_IDX_ACTIVE": 10.0}
     rows = [[1, kname, k, 7 * v] for k, v in second.items()]
     rows += [[2, kname, k, v] for k, v in second.items()]
@@ -77,7 +79,7 @@ def test_counters_summary(tmp_path):
     out = res.stdout
     assert "| MFMA FLOPs / algorithmic FLOPs | 1.0000 |" in out
     assert "= 50.0 %" in out                      # 500 busy cycles per SIMD of 1000
-    assert "| non-MFMA VALU instructions per MFMA | 3.00 |" in out
+    assert f"| non-MFMA VALU instructions per MFMA ({shape}) | 3.00 |" in out
     assert f"{flops / 1e-3 / 1e12:.1f}" in out    # 1 ms, the second launch only
     assert f"= 1.00 x algorithmic {alg:,}" in out
 
