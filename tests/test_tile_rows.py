@@ -122,3 +122,27 @@ def test_more_heads_than_the_reference_grid_limit(d, causal):
         sl = (slice(bi, bi + 1), slice(0, 1))
         ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("b,h,n,causal", [(4, 16, 1000, False), (2, 16, 3100, True)])
+@pytest.mark.parametrize("scale", [0.3, -0.2, 0.0, 1.5])
+def test_pingpong16_scales_and_lse(b, h, n, causal, scale):
+    """The d=128 ping-pong row (16x16x32 MFMAs) with custom, negative (Q negated), zero and
+    large softmax scales, O and the row LSE, against the oracle."""
+    import fa
+    from fa import native
+
+    tile = native.tile_config(128, causal, "opt", n, b, h)
+    got = (tile["block_q"], tile["block_k"], tile["waves"], tile["lds_bytes"])
+    print(f"case B={b} H={h} N={n} causal={causal} scale={scale} tile={got}", flush=True)
+    assert got == PP128
+    g = torch.Generator().manual_seed(int(1000 * scale) + n)
+    q, k, v = (torch.randn(b, h, n, 128, generator=g).half() for _ in range(3))
+    out, lse = fa.forward_lse(q.cuda(), k.cuda(), v.cuda(), causal=causal, softmax_scale=scale)
+    out, lse = out.cpu(), lse.cpu()
+    for bi, hi in {(0, 0), (b - 1, h - 1)}:
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal, scale=scale)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+        ref_lse = orc.lse_fp32(q[sl], k[sl], causal=causal, scale=scale)
+        torch.testing.assert_close(lse[sl], ref_lse, atol=2e-3, rtol=0)
