@@ -57,55 +57,75 @@ constexpr int mfma32_c_col(int lane) { return lane & 31; }
 constexpr int mfma16_c_row(int lane, int r) { return 4 * (lane >> 4) + r; }
 constexpr int mfma16_c_col(int lane) { return lane & 15; }
 
-// ---- The 16x16x32 MFMA path (D = 128, 256-byte rows, 32-key tiles) --------------------------
+// ---- The 16x16x32 MFMA path (flash_fwd_pingpong16; D = 128 with 32-key tiles, D = 64 with
+// 64-key tiles; d is the head dim, rows are 2d bytes) ------------------------------------------
 // Key blocks: the 16 keys of score block kb (the M rows of its MFMAs) are tile rows
-// 8kb + {0..7} and 8kb + {16..23}, i.e. row m16_key(kb, i) for M index i. A 16-lane group of a
-// K fragment read then spans both 4 KiB halves of the tile, and so does each half-wave of a
-// V^T read. Measured on MI355X (8 waves per CU, conflict-free patterns): ds_read_b128 at
-// 256 B per CU cycle with this split against 128 B with contiguous 16-row blocks (all lanes in
-// one 4 KiB half); ds_read_b64_tr_b16 at 160 B against 132 B (and 64 B for the 32x32x16 V^T
-// pattern, four lanes groups on the same four rows).
-constexpr int m16_key(int kb, int i) { return 8 * kb + (i & 7) + 16 * ((i >> 3) & 1); }
+// 32*(kb/2) + 8*(kb%2) + {0..7, 16..23}, i.e. row m16_key(kb, i) for M index i: each 32-key
+// group of the tile holds two key blocks interleaved by 8 rows. A 16-lane group of a K operand
+// then spans both 4 KiB halves of a D = 128 tile, and so does each half-wave of a V^T read.
+// Measured on MI355X (8 waves per CU, conflict-free patterns): ds_read_b128 at 256 B per CU
+// cycle with this split against 128 B with contiguous 16-row blocks (all lanes in one 4 KiB
+// half); ds_read_b64_tr_b16 at 160 B against 132 B (and 64 B for the 32x32x16 V^T pattern,
+// four lanes groups on the same four rows).
+constexpr int m16_key(int kb, int i) {
+    return 32 * (kb >> 1) + 8 * (kb & 1) + (i & 7) + 16 * ((i >> 3) & 1);
+}
 
-// LDS swizzle of these tiles: row_xor_m16 = 2*(row%8) + (row/16)%2. K reads (16 lanes: the 16
-// rows of a key block, one logical chunk) see 16 distinct values; V^T reads (32 lanes: 8 rows,
-// 8 even or 8 odd values, logical chunks 2c and 2c+1) land on 16 distinct chunks. Rows 8
-// apart within a key block's half share the value, so the kb = 1 block and the second V^T read
-// are immediate offsets (+8 rows).
-constexpr int row_xor_m16(int row) { return ((row & 7) << 1) | ((row >> 4) & 1); }
-constexpr int swizzle_chunk_m16(int row, int chunk) { return chunk ^ row_xor_m16(row); }
-constexpr int tile_offset_m16(int row, int chunk) {
-    return row * 256 + 16 * swizzle_chunk_m16(row, chunk);
+// LDS swizzle of the V tiles of this path. D = 128: row_xor_m16 = 2*(row%8) + (row/16)%2. A V^T
+// read (32 lanes: 8 rows aligned to 8, logical chunks 2c and 2c+1, 32 bytes per row) sees the 8
+// even or the 8 odd values, which put the 8 row pieces on 16 distinct chunks. D = 64 (two rows
+// per 256-byte bank line): row_xor_m16 = 2*((row/2)%4) moves the 32-byte piece of each of the 4
+// even rows (banks 0-31) and of the 4 odd rows (banks 32-63) to its own quarter. In both, rows
+// 8 apart within a key block's half and rows 32 apart share the value, so the second read of a
+// fragment and the next 32-key group are immediate offsets.
+constexpr int row_xor_m16(int row, int d) {
+    return d >= 128 ? (((row & 7) << 1) | ((row >> 4) & 1)) : (((row >> 1) & 3) << 1);
+}
+constexpr int swizzle_chunk_m16(int row, int chunk, int d) { return chunk ^ row_xor_m16(row, d); }
+constexpr int tile_offset_m16(int row, int chunk, int d) {
+    return row * 2 * d + 16 * swizzle_chunk_m16(row, chunk, d);
 }
 
 // K tiles of this path use their own LDS layout: the K operand of MFMA step (kb, dc) is read
-// with exactly the lane addresses of the 32x32x16 path's K fragment kk = 4kb + dc,
-// tile_offset(lane % 32, 2kk + lane / 32, 256), whose ds_read_b128 pattern measures
-// conflict-free (the direct 16x16x32 pattern, four lane groups on four chunks of the same 16
-// rows, costs 4 conflict cycles per read on MI355X). Lane l must receive key row
-// m16_key(kb, l % 16), 16-byte chunk m16_kchunk(dc, l / 16): the MFMA's k slots 8g..8g+7 of
-// lane group g are features 32g + 8dc .. +7, and the Q^T operand uses the same order.
-// m16_kslot_row / m16_kslot_chunk give the element that 16-byte LDS slot `slot` holds.
-constexpr int m16_kchunk(int dc, int grp) { return 4 * grp + dc; }
-constexpr int m16_kslot_t(int slot) { return (slot & 15) ^ row_xor(slot >> 4, 256); }
-constexpr int m16_kslot_row(int slot) {
-    return m16_key(m16_kslot_t(slot) >> 3, (slot >> 4) & 15);
+// with exactly the lane addresses of the 32x32x16 path's K fragment (nb, kk) with nb = kb / 2,
+// kk = (kb % 2) * DC + dc (DC = d / 32), tile_offset(32 nb + lane % 32, 2kk + lane / 32, 2d),
+// whose ds_read_b128 pattern measures conflict-free (the direct 16x16x32 pattern, four lane
+// groups on four chunks of the same 16 rows, costs 4 conflict cycles per read on MI355X). Lane
+// l must receive key row m16_key(kb, l % 16), 16-byte chunk m16_kchunk(dc, l / 16, d): the
+// MFMA's k slots 8g..8g+7 of lane group g are features 8 * m16_kchunk(dc, g, d) .. +7, and the
+// Q^T operand uses the same order. m16_kslot_row / m16_kslot_chunk give the element that
+// 16-byte LDS slot `slot` holds.
+// (For d = 64 the two lane groups a DMA request covers, g and g + 2, get adjacent chunk pairs,
+// so that each request reads whole 64-byte pieces of a K row.)
+constexpr int m16_kchunk(int dc, int grp, int d) {
+    return d >= 128 ? 4 * grp + dc : 4 * (grp & 1) + 2 * (grp >> 1) + dc;
 }
-constexpr int m16_kslot_chunk(int slot) {
-    return m16_kchunk((m16_kslot_t(slot) >> 1) & 3, (slot >> 8) + 2 * (m16_kslot_t(slot) & 1));
+constexpr int m16_kslot_t(int slot, int d) {
+    return (slot % (d / 8)) ^ row_xor(slot / (d / 8), 2 * d);
+}
+constexpr int m16_kslot_kb(int slot, int d) {  // 2 nb + kk / DC
+    return 2 * ((slot / (d / 8)) >> 5) + (m16_kslot_t(slot, d) >> 1) / (d / 32);
+}
+constexpr int m16_kslot_row(int slot, int d) {
+    return m16_key(m16_kslot_kb(slot, d), (slot / (d / 8)) & 15);
+}
+constexpr int m16_kslot_chunk(int slot, int d) {
+    return m16_kchunk((m16_kslot_t(slot, d) >> 1) % (d / 32),
+                      (((slot / (d / 8)) >> 4) & 1) + 2 * (m16_kslot_t(slot, d) & 1), d);
 }
 
-// S^T = K Q^T of a wave (32 queries) and a 32-key tile in four 16x16 blocks (kb, qb):
-// accumulator r of block (kb, qb) in `lane` is key st16_key(lane, kb, r) of the tile and query
+// S^T = K Q^T of a wave (32 queries) and a key tile in 16x16 blocks (kb, qb): accumulator r
+// of block (kb, qb) in `lane` is key st16_key(lane, kb, r) of the tile and query
 // st16_query(lane, qb) of the wave. Each lane thus holds 4 keys of 2 queries per key block.
 constexpr int st16_key(int lane, int kb, int r) { return m16_key(kb, mfma16_c_row(lane, r)); }
 constexpr int st16_query(int lane, int qb) { return 16 * qb + (lane & 15); }
 
-// Key carried by operand slot i (0..7) of the O^T += V^T P^T MFMA in `lane`: slots 0..3 are
-// the lane's scores of key block 0, slots 4..7 those of block 1, so P^T of query block qb is
-// the lane's own 8 exponentials in order (no shuffle), and the V^T operand reads these keys.
-// The key depends on lane / 16 and i only, as the MFMA's shared k index requires.
-constexpr int pv16_key(int lane, int i) { return st16_key(lane, i >> 2, i & 3); }
+// Key carried by operand slot i (0..7) of k step t (32 keys) of the O^T += V^T P^T MFMA in
+// `lane`: slots 0..3 are the lane's scores of key block 2t, slots 4..7 those of block 2t + 1,
+// so P^T of query block qb is the lane's own 8 exponentials in order (no shuffle), and the
+// V^T operand reads these keys. The key depends on lane / 16, t and i only, as the MFMA's
+// shared k index requires.
+constexpr int pv16_key(int lane, int t, int i) { return st16_key(lane, 2 * t + (i >> 2), i & 3); }
 
 // ---- Transposed operand reads (ds_read_b64_tr_b16) ------------------------------------------
 // Within each group of 16 lanes, the instruction loads a 4 x 16 block of 16-bit values

@@ -133,9 +133,10 @@ __global__ __launch_bounds__(512) void probe_lds_kernel(float* out, unsigned lon
     const unsigned v16plain = v16row * 256 + 8 * (lane & 3);
     // MODE 5 / 6: the layout the 16x16x32 kernel uses (fa::geom::m16_key / tile_offset_m16:
     // key blocks split over both 4 KiB halves of the tile).
-    const unsigned k5base = fa::geom::tile_offset_m16(fa::geom::m16_key(0, lane & 15), lane >> 4);
-    const int v6row = fa::geom::pv16_key(lane, 0) + fa::geom::tr16_row(lane);
-    const unsigned v6base = fa::geom::tile_offset_m16(v6row, fa::geom::tr16_col(lane) >> 3) +
+    const unsigned k5base =
+        fa::geom::tile_offset_m16(fa::geom::m16_key(0, lane & 15), lane >> 4, 128);
+    const int v6row = fa::geom::pv16_key(lane, 0, 0) + fa::geom::tr16_row(lane);
+    const unsigned v6base = fa::geom::tile_offset_m16(v6row, fa::geom::tr16_col(lane) >> 3, 128) +
                             2 * (fa::geom::tr16_col(lane) & 7);
     unsigned acc = 0;
     const unsigned long long s0 = __builtin_amdgcn_s_memtime();

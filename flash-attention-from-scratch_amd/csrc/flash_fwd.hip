@@ -121,7 +121,8 @@ namespace g = fa::geom;
 // interleaved with the softmax of tile j in each wave), PINGPONG (flash_fwd_pingpong: two
 // groups of waves alternate between an MFMA-only phase and a softmax phase), KSPLIT
 // (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles), PINGPONG16
-// (flash_fwd_pingpong16: the ping-pong schedule on 16x16x32 MFMAs).
+// (flash_fwd_pingpong16: the ping-pong schedule on 16x16x32 MFMAs; the table's long-sequence
+// rows; PINGPONG stays for A/B builds).
 enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3, PINGPONG16 = 4 };
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
@@ -166,10 +167,10 @@ struct TileDma {
             int row = slot / T::CPR;
             int chunk;
             if (KLAYOUT) {
-                row = g::m16_kslot_row(slot);
-                chunk = g::m16_kslot_chunk(slot);
+                row = g::m16_kslot_row(slot, T::D);
+                chunk = g::m16_kslot_chunk(slot, T::D);
             } else {
-                chunk = T::M16 ? g::swizzle_chunk_m16(row, slot % T::CPR)
+                chunk = T::M16 ? g::swizzle_chunk_m16(row, slot % T::CPR, T::D)
                                : g::swizzle_chunk(row, slot % T::CPR, T::ROW_BYTES);
             }
             voff[it] = row * T::ROW_BYTES + 16 * chunk;
@@ -990,6 +991,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
 #define FA_PP_MASKED_STEADY 1
 #endif
 
+#ifndef FA_PP_EXPS_FIRST
+#define FA_PP_EXPS_FIRST 1
+#endif
+
 // Scheduler pattern: N times {R DS reads, V VALU instructions} (sched_group_barrier masks
 // 0x100 DS read, 0x002 VALU | 0x400 transcendental).
 #ifndef FA_PP_READS_PER
@@ -1033,6 +1038,27 @@ __device__ __forceinline__ void softmax_optimistic(const f32x16 (&s)[T::NB], flo
                                                    f16x8 (&p)[T::NB][2]) {
     float sum0 = 0.0F;
     float sum1 = 0.0F;
+#if FA_PP_EXPS_FIRST
+    // All exponentials of the tile first, then the packs and sums (a pack right behind the
+    // exponentials it reads waits on their latency).
+    float e[T::NB][16];
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[nb][r] = exp2_fast(fmaf(s[nb][r], scale_log2, -m_run));
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) {
+        p[nb][0] = pack8(e[nb][0], e[nb][1], e[nb][2], e[nb][3], e[nb][4], e[nb][5], e[nb][6],
+                         e[nb][7]);
+        p[nb][1] = pack8(e[nb][8], e[nb][9], e[nb][10], e[nb][11], e[nb][12], e[nb][13],
+                         e[nb][14], e[nb][15]);
+    }
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb) {
+        sum0 = sum8_f16(p[nb][0], sum0);
+        sum1 = sum8_f16(p[nb][1], sum1);
+    }
+#else
 #pragma unroll
     for (int nb = 0; nb < T::NB; ++nb) {
         float e[16];
@@ -1043,6 +1069,7 @@ __device__ __forceinline__ void softmax_optimistic(const f32x16 (&s)[T::NB], flo
         sum0 = sum8_f16(p[nb][0], sum0);
         sum1 = sum8_f16(p[nb][1], sum1);
     }
+#endif
     const float sum = sum0 + sum1;
     overflow = wave_any(!(sum < INFINITY));
     const float l_new = l_run + sum;
@@ -1260,17 +1287,18 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
     FA_CLOCK_END();
 }
 
-// ---- ping-pong on 16x16x32 MFMAs (D = 128) ----------------------------------------------------
+// ---- ping-pong on 16x16x32 MFMAs (D = 128 with 32-key tiles, D = 64 with 64-key tiles) --------
 // The schedule and buffer protocol of flash_fwd_pingpong, with the matrix work on
 // v_mfma_f32_16x16x32_f16 (two of half the FLOPs per 32x32x16). On MI355X, which runs this
 // kernel at its power limit, a stream of 16x16x32 MFMAs on random fp16 data sustains about
 // 20 % more FLOPS than the same FLOPs in 32x32x16 MFMAs: the chip holds a higher clock.
-// Per wave (32 queries) and 32-key tile: S^T in four 16x16 blocks s[kb][qb] (keys 16kb..,
-// queries 16qb..), so a lane holds 4 keys of each of two queries (lane % 16 and 16 + lane % 16)
-// and keeps a running max and sum per query block. P^T of query block qb is the lane's own
-// 8 exponentials, in the key order fa::geom::pv16_key that the V^T operand reads. O^T in 16
-// blocks oacc[db][qb] (features 16db.., queries 16qb..). The LDS tiles use the swizzle
-// fa::geom::row_xor_m16, conflict-free for these read patterns.
+// Per wave (32 queries) and key tile: S^T in 16x16 blocks s[kb][qb] (key block kb =
+// fa::geom::m16_key rows, queries 16qb..), so a lane holds 4 keys of each of two queries
+// (lane % 16 and 16 + lane % 16) and keeps a running max and sum per query block. P^T of query
+// block qb and 32-key step t is the lane's own 8 exponentials, in the key order
+// fa::geom::pv16_key that the V^T operand reads. O^T in blocks oacc[db][qb] (features 16db..,
+// queries 16qb..). V tiles use the swizzle fa::geom::row_xor_m16; K tiles are stored so that
+// the K operand is read at the 32x32x16 path's conflict-free addresses (m16_kslot_row).
 // Fragment reads and softmax VALU of the softmax phase: N times {R reads, V VALU} (as
 // FA_PP_READS_PER / FA_PP_VALU_PER for flash_fwd_pingpong); R must divide the 24 reads.
 #ifndef FA_PP16_READS_PER
@@ -1279,95 +1307,120 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 #ifndef FA_PP16_VALU_PER
 #define FA_PP16_VALU_PER 16
 #endif
-namespace m16 {
-constexpr int KB = 2;  // 16-key blocks per 32-key tile
-constexpr int QB = 2;  // 16-query blocks per wave
-constexpr int DC = 4;  // 32-deep MFMA steps over D = 128
-constexpr int DB = 8;  // 16-wide feature blocks over D = 128
-constexpr int ROW = 256;  // bytes per K/V row
-}  // namespace m16
+// Per-tile geometry of the 16x16x32 path: D = 128 with 32-key tiles or D = 64 with 64-key
+// tiles; either way 32 MFMAs of each kind per wave and tile and 24 fragment reads.
+template <class T>
+struct M16 {
+    static constexpr int D = T::D;
+    static constexpr int KB = T::BC / 16;  // 16-key blocks per tile
+    static constexpr int QB = 2;           // 16-query blocks per wave
+    static constexpr int DC = D / 32;      // 32-deep MFMA steps over D
+    static constexpr int DB = D / 16;      // 16-wide feature blocks over D
+    static constexpr int KS = T::BC / 32;  // 32-key steps of the P.V product
+    static constexpr int ROW = 2 * D;      // bytes per K/V row
+    static constexpr int READS = KB * DC + 2 * KS * DB;
+    static_assert(KB * QB * DC == 16 && DB * QB * KS == 16, "16 + 16 MFMAs per wave and tile");
+};
 
 // Lane-dependent LDS offsets: K fragment (kb, dc) at the 32x32x16 path's fragment address for
-// kk = 4kb + dc (the K tile's own layout, fa::geom::m16_kslot_row); V^T fragment db: the 4 rows
-// pv16_key(lane, 0..3) (via the tr16 addressing of a 4-row block), 16 feature columns from
-// 16db (the second read, keys pv16_key(lane, 4..7), is 8 rows further).
+// nb = kb / 2, kk = (kb % 2) * DC + dc (the K tile's own layout, fa::geom::m16_kslot_row);
+// V^T fragment db: the 4 rows pv16_key(lane, 0, 0..3) (via the tr16 addressing of a 4-row
+// block), 16 feature columns from 16db (the second read, keys pv16_key(lane, 0, 4..7), is 8
+// rows further; k step t is 32 rows further).
+template <class T>
 struct Frag16 {
-    int koff[m16::KB][m16::DC];
-    int voff[m16::DB];
+    using G = M16<T>;
+    int koff[G::KB][G::DC];
+    int voff[G::DB];
     __device__ __forceinline__ explicit Frag16(int lane) {
 #pragma unroll
-        for (int kb = 0; kb < m16::KB; ++kb)
+        for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-            for (int dc = 0; dc < m16::DC; ++dc)
-                koff[kb][dc] = g::tile_offset(lane & 31, 2 * (4 * kb + dc) + (lane >> 5), m16::ROW);
+            for (int dc = 0; dc < G::DC; ++dc)
+                koff[kb][dc] = g::tile_offset(32 * (kb >> 1) + (lane & 31),
+                                              2 * ((kb & 1) * G::DC + dc) + (lane >> 5), G::ROW);
 #pragma unroll
-        for (int db = 0; db < m16::DB; ++db) {
-            const int row = g::pv16_key(lane, 0) + g::tr16_row(lane);
+        for (int db = 0; db < G::DB; ++db) {
+            const int row = g::pv16_key(lane, 0, 0) + g::tr16_row(lane);
             const int c = 16 * db + g::tr16_col(lane);  // halves
-            voff[db] = g::tile_offset_m16(row, c >> 3) + 2 * (c & 7);
+            voff[db] = g::tile_offset_m16(row, c >> 3, G::D) + 2 * (c & 7);
         }
     }
 };
 
 // Q^T operands: qf[qb][dc] holds Q[qw + 16qb + lane%16][8 * m16_kchunk(dc, lane/16) .. +7],
 // the feature order of the K operand.
+template <class T>
 __device__ __forceinline__ void load_q16(const f16* qh, int qw, int n, int lane, int negate_q,
-                                         f16x8 (&qf)[m16::QB][m16::DC]) {
+                                         f16x8 (&qf)[M16<T>::QB][M16<T>::DC]) {
+    using G = M16<T>;
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb) {
+    for (int qb = 0; qb < G::QB; ++qb) {
         const int row = min(qw + 16 * qb + (lane & 15), n - 1);
-        const f16* src = qh + static_cast<size_t>(row) * 128;
+        const f16* src = qh + static_cast<size_t>(row) * G::D;
 #pragma unroll
-        for (int dc = 0; dc < m16::DC; ++dc) {
-            qf[qb][dc] = *reinterpret_cast<const f16x8*>(src + 8 * g::m16_kchunk(dc, lane >> 4));
+        for (int dc = 0; dc < G::DC; ++dc) {
+            qf[qb][dc] =
+                *reinterpret_cast<const f16x8*>(src + 8 * g::m16_kchunk(dc, lane >> 4, G::D));
             if (negate_q) qf[qb][dc] = -qf[qb][dc];
         }
     }
 }
 
-// K fragments of a tile (8 ds_read_b128) and V^T fragments (16 ds_read_b64_tr_b16).
-__device__ __forceinline__ void load_k16(const char* kl, const Frag16& fr,
-                                         f16x8 (&kf)[m16::KB][m16::DC]) {
+// K fragments of a tile (KB * DC ds_read_b128) and V^T fragments (2 * KS * DB
+// ds_read_b64_tr_b16).
+template <class T>
+__device__ __forceinline__ void load_k16(const char* kl, const Frag16<T>& fr,
+                                         f16x8 (&kf)[M16<T>::KB][M16<T>::DC]) {
+    using G = M16<T>;
 #pragma unroll
-    for (int kb = 0; kb < m16::KB; ++kb)
+    for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-        for (int dc = 0; dc < m16::DC; ++dc)
+        for (int dc = 0; dc < G::DC; ++dc)
             kf[kb][dc] = *reinterpret_cast<const f16x8*>(kl + fr.koff[kb][dc]);
 }
-__device__ __forceinline__ void load_v16(const char* vl, const Frag16& fr,
-                                         f16x8 (&vf)[m16::DB]) {
+template <class T>
+__device__ __forceinline__ void load_v16(const char* vl, const Frag16<T>& fr,
+                                         f16x8 (&vf)[M16<T>::KS][M16<T>::DB]) {
+    using G = M16<T>;
 #pragma unroll
-    for (int db = 0; db < m16::DB; ++db) {
-        const f16x4 lo = lds_read_tr16(vl + fr.voff[db]);
-        const f16x4 up = lds_read_tr16(vl + fr.voff[db] + 8 * m16::ROW);
-        vf[db] = f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-    }
+    for (int t = 0; t < G::KS; ++t)
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+            const char* base = vl + fr.voff[db] + 32 * t * G::ROW;
+            const f16x4 lo = lds_read_tr16(base);
+            const f16x4 up = lds_read_tr16(base + 8 * G::ROW);
+            vf[t][db] = f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+        }
 }
 
 // S^T = K Q^T of one tile (the first one, before the steady phases).
-__device__ __forceinline__ void qk16(const char* kl, const Frag16& fr,
-                                     const f16x8 (&qf)[m16::QB][m16::DC],
-                                     f32x4 (&s)[m16::KB][m16::QB]) {
-    f16x8 kf[m16::KB][m16::DC];
-    load_k16(kl, fr, kf);
+template <class T>
+__device__ __forceinline__ void qk16(const char* kl, const Frag16<T>& fr,
+                                     const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
+                                     f32x4 (&s)[M16<T>::KB][M16<T>::QB]) {
+    using G = M16<T>;
+    f16x8 kf[G::KB][G::DC];
+    load_k16<T>(kl, fr, kf);
 #pragma unroll
-    for (int kb = 0; kb < m16::KB; ++kb)
+    for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < m16::QB; ++qb) {
+        for (int qb = 0; qb < G::QB; ++qb) {
             s[kb][qb] = f32x4{};
 #pragma unroll
-            for (int dc = 0; dc < m16::DC; ++dc) s[kb][qb] = mfma16(kf[kb][dc], qf[qb][dc], s[kb][qb]);
+            for (int dc = 0; dc < G::DC; ++dc) s[kb][qb] = mfma16(kf[kb][dc], qf[qb][dc], s[kb][qb]);
         }
 }
 
 // Keys >= n, and (causal) keys right of the query, get -inf.
-template <bool CAUSAL>
-__device__ __forceinline__ void mask16(f32x4 (&s)[m16::KB][m16::QB], int kt, int n, int qw,
-                                       int lane) {
+template <class T, bool CAUSAL>
+__device__ __forceinline__ void mask16(f32x4 (&s)[M16<T>::KB][M16<T>::QB], int kt, int n,
+                                       int qw, int lane) {
+    using G = M16<T>;
 #pragma unroll
-    for (int kb = 0; kb < m16::KB; ++kb)
+    for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < m16::QB; ++qb)
+        for (int qb = 0; qb < G::QB; ++qb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = kt + g::st16_key(lane, kb, r);
@@ -1377,113 +1430,152 @@ __device__ __forceinline__ void mask16(f32x4 (&s)[m16::KB][m16::QB], int kt, int
             }
 }
 
+// P^T operand slot i of k step t of query block qb: score accumulator i % 4 of key block
+// 2t + i / 4 (fa::geom::pv16_key).
+template <class T>
+__device__ __forceinline__ f16x8 pack16(const float (&e)[M16<T>::KB][4], int t) {
+    return pack8(e[2 * t][0], e[2 * t][1], e[2 * t][2], e[2 * t][3], e[2 * t + 1][0],
+                 e[2 * t + 1][1], e[2 * t + 1][2], e[2 * t + 1][3]);
+}
+
 // Optimistic softmax against the running max (as softmax_optimistic): P in fp16 and l += row
 // sums, unless some p overflowed fp16, in which case `overflow` is set (wave-uniform) and the
-// caller redoes the tile exactly.
-__device__ __forceinline__ void softmax16_optimistic(const f32x4 (&s)[m16::KB][m16::QB],
+// caller redoes the tile exactly. All exponentials are issued first, then the packs and the two
+// row sums (interleaved v_dot2 chains): a pack or sum right after the exponentials it reads
+// would wait on their latency.
+template <class T>
+__device__ __forceinline__ void softmax16_optimistic(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
                                                      float scale_log2,
-                                                     const float (&m_run)[m16::QB],
-                                                     float (&l_run)[m16::QB], bool& overflow,
-                                                     f16x8 (&p)[m16::QB]) {
-    // All 16 exponentials first, then the packs and the two row sums: a pack or sum right after
-    // the exponentials it reads would wait on their latency.
-    float e[m16::QB][8];
+                                                     const float (&m_run)[M16<T>::QB],
+                                                     float (&l_run)[M16<T>::QB], bool& overflow,
+                                                     f16x8 (&p)[M16<T>::QB][M16<T>::KS]) {
+    using G = M16<T>;
+    float e[G::QB][G::KB][4];
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb)
+    for (int qb = 0; qb < G::QB; ++qb)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            e[qb][i] = exp2_fast(fmaf(s[i >> 2][qb][i & 3], scale_log2, -m_run[qb]));
-    float sum[m16::QB] = {0.0F, 0.0F};
+        for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb)
-        p[qb] = pack8(e[qb][0], e[qb][1], e[qb][2], e[qb][3], e[qb][4], e[qb][5], e[qb][6],
-                      e[qb][7]);
-    // The two sums as interleaved v_dot2 chains.
+            for (int r = 0; r < 4; ++r)
+                e[qb][kb][r] = exp2_fast(fmaf(s[kb][qb][r], scale_log2, -m_run[qb]));
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+        for (int t = 0; t < G::KS; ++t) p[qb][t] = pack16<T>(e[qb], t);
+    float sum[G::QB] = {0.0F, 0.0F};
     const f16x2 one = {static_cast<f16>(1.0F), static_cast<f16>(1.0F)};
 #define FA_SUM2(K)                                                                              \
-    for (int qb = 0; qb < m16::QB; ++qb)                                                       \
-        sum[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(p[qb], p[qb], 2 * (K),        \
+    for (int qb = 0; qb < G::QB; ++qb)                                                         \
+        sum[qb] = __builtin_amdgcn_fdot2(__builtin_shufflevector(p[qb][t], p[qb][t], 2 * (K),  \
                                                                  2 * (K) + 1),                  \
                                          one, sum[qb], false);
-    FA_SUM2(0)
-    FA_SUM2(1)
-    FA_SUM2(2)
-    FA_SUM2(3)
+#pragma unroll
+    for (int t = 0; t < G::KS; ++t) {
+        FA_SUM2(0)
+        FA_SUM2(1)
+        FA_SUM2(2)
+        FA_SUM2(3)
+    }
 #undef FA_SUM2
     overflow = wave_any(!(sum[0] < INFINITY && sum[1] < INFINITY));
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb) l_run[qb] = overflow ? l_run[qb] : l_run[qb] + sum[qb];
+    for (int qb = 0; qb < G::QB; ++qb) l_run[qb] = overflow ? l_run[qb] : l_run[qb] + sum[qb];
 }
 
 // Exact online softmax of one tile (as softmax_tile): the tile max of a query spans the four
 // lanes lane % 16 + 16*i that hold its keys.
 template <class T>
-__device__ __forceinline__ void softmax16_tile(const f32x4 (&s)[m16::KB][m16::QB],
-                                               float scale_log2, float (&m_run)[m16::QB],
-                                               float (&l_run)[m16::QB], float (&alpha)[m16::QB],
-                                               bool& rescale, f16x8 (&p)[m16::QB]) {
-    float mx[m16::QB];
+__device__ __forceinline__ void softmax16_tile(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
+                                               float scale_log2, float (&m_run)[M16<T>::QB],
+                                               float (&l_run)[M16<T>::QB],
+                                               float (&alpha)[M16<T>::QB], bool& rescale,
+                                               f16x8 (&p)[M16<T>::QB][M16<T>::KS]) {
+    using G = M16<T>;
+    float mx[G::QB];
     bool grow = false;
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb) {
+    for (int qb = 0; qb < G::QB; ++qb) {
         float x = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x = fmaxf(x, s[i >> 2][qb][i & 3]);
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x = fmaxf(x, s[kb][qb][r]);
         mx[qb] = max_xor32(max_xor16(x)) * scale_log2;
         grow = grow || (T::LAZY ? (mx[qb] > m_run[qb] + 8.0F) : (mx[qb] > m_run[qb]));
     }
     rescale = wave_any(grow);
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb) {
+    for (int qb = 0; qb < G::QB; ++qb) {
         const float m_new = rescale ? fmaxf(m_run[qb], mx[qb]) : m_run[qb];
         const float m_use = (m_new == -INFINITY) ? 0.0F : m_new;
         alpha[qb] = exp2_fast(m_run[qb] - m_use);
         m_run[qb] = m_new;
-        float e[8];
+        float e[G::KB][4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = exp2_fast(fmaf(s[i >> 2][qb][i & 3], scale_log2, -m_use));
-        p[qb] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
-        l_run[qb] = (rescale ? l_run[qb] * alpha[qb] : l_run[qb]) + sum8_f16(p[qb], 0.0F);
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) e[kb][r] = exp2_fast(fmaf(s[kb][qb][r], scale_log2, -m_use));
+        float sum = 0.0F;
+#pragma unroll
+        for (int t = 0; t < G::KS; ++t) {
+            p[qb][t] = pack16<T>(e, t);
+            sum = sum8_f16(p[qb][t], sum);
+        }
+        l_run[qb] = (rescale ? l_run[qb] * alpha[qb] : l_run[qb]) + sum;
     }
 }
 
-__device__ __forceinline__ void rescale16(f32x4 (&oacc)[m16::DB][m16::QB],
-                                          const float (&alpha)[m16::QB]) {
+template <class T>
+__device__ __forceinline__ void rescale16(f32x4 (&oacc)[M16<T>::DB][M16<T>::QB],
+                                          const float (&alpha)[M16<T>::QB]) {
 #pragma unroll
-    for (int db = 0; db < m16::DB; ++db)
+    for (int db = 0; db < M16<T>::DB; ++db)
 #pragma unroll
-        for (int qb = 0; qb < m16::QB; ++qb) oacc[db][qb] *= alpha[qb];
+        for (int qb = 0; qb < M16<T>::QB; ++qb) oacc[db][qb] *= alpha[qb];
 }
 
-__device__ __forceinline__ void pv16(const f16x8 (&vf)[m16::DB], const f16x8 (&p)[m16::QB],
-                                     f32x4 (&oacc)[m16::DB][m16::QB]) {
+template <class T>
+__device__ __forceinline__ void pv16(const f16x8 (&vf)[M16<T>::KS][M16<T>::DB],
+                                     const f16x8 (&p)[M16<T>::QB][M16<T>::KS],
+                                     f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
+    using G = M16<T>;
 #pragma unroll
-    for (int db = 0; db < m16::DB; ++db)
+    for (int t = 0; t < G::KS; ++t)
 #pragma unroll
-        for (int qb = 0; qb < m16::QB; ++qb) oacc[db][qb] = mfma16(vf[db], p[qb], oacc[db][qb]);
+        for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+            for (int qb = 0; qb < G::QB; ++qb)
+                oacc[db][qb] = mfma16(vf[t][db], p[qb][t], oacc[db][qb]);
 }
 
-// Matrix phase: S^T_{j+1} (16 MFMAs, four independent chains of 4) alternating with
-// O^T += V_j^T P_j^T (16 MFMAs, independent); `mid` (the refill) after the first 8.
-template <class Mid>
-__device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[m16::KB][m16::DC],
-                                               const f16x8 (&qf)[m16::QB][m16::DC],
-                                               const f16x8 (&vf)[m16::DB],
-                                               const f16x8 (&p)[m16::QB],
-                                               f32x4 (&s)[m16::KB][m16::QB],
-                                               f32x4 (&oacc)[m16::DB][m16::QB], Mid&& mid) {
+// Matrix phase: S^T_{j+1} (16 MFMAs: KB*QB independent chains of DC, step i on chain i % (KB*QB))
+// alternating with O^T += V_j^T P_j^T (16 MFMAs, independent); `mid` (the refill) after the
+// first 8.
+template <class T, class Mid>
+__device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16<T>::DC],
+                                               const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
+                                               const f16x8 (&vf)[M16<T>::KS][M16<T>::DB],
+                                               const f16x8 (&p)[M16<T>::QB][M16<T>::KS],
+                                               f32x4 (&s)[M16<T>::KB][M16<T>::QB],
+                                               f32x4 (&oacc)[M16<T>::DB][M16<T>::QB],
+                                               Mid&& mid) {
+    using G = M16<T>;
+    constexpr int NCH = G::KB * G::QB;  // QK chains
 #pragma unroll
-    for (int kb = 0; kb < m16::KB; ++kb)
+    for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < m16::QB; ++qb) s[kb][qb] = f32x4{};
+        for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = f32x4{};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int kb = (i >> 1) & 1;
-        const int qs = i & 1;
-        const int dc = i >> 2;
+        const int ch = i % NCH;
+        const int kb = ch / G::QB;
+        const int qs = ch % G::QB;
+        const int dc = i / NCH;
         s[kb][qs] = mfma16(kf[kb][dc], qf[qs][dc], s[kb][qs]);
-        const int db = i >> 1;
-        oacc[db][qs] = mfma16(vf[db], p[qs], oacc[db][qs]);
+        const int qv = i % G::QB;
+        const int db = (i / G::QB) % G::DB;
+        const int t = i / (G::QB * G::DB);
+        oacc[db][qv] = mfma16(vf[t][db], p[qv][t], oacc[db][qv]);
         __builtin_amdgcn_sched_barrier(0);  // keep the alternation
         if (i == 3) {
             mid();
@@ -1494,22 +1586,24 @@ __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[m16::KB][m16::D
 
 // O = acc / l as fp16 for the lane's two queries (if < n), and the natural-log LSE if lse_h is
 // not null. The lane holds features 16db + 4*(lane/16) + 0..3: one 8-byte store per db.
+template <class T>
 __device__ __forceinline__ void store16(f16* oh, float* lse_h, int qw, int n, int lane,
-                                        const float (&m_run)[m16::QB],
-                                        const float (&l_run)[m16::QB],
-                                        const f32x4 (&oacc)[m16::DB][m16::QB]) {
-    float l_tot[m16::QB];
+                                        const float (&m_run)[M16<T>::QB],
+                                        const float (&l_run)[M16<T>::QB],
+                                        const f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
+    using G = M16<T>;
+    float l_tot[G::QB];
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb) l_tot[qb] = sum_xor32(sum_xor16(l_run[qb]));
+    for (int qb = 0; qb < G::QB; ++qb) l_tot[qb] = sum_xor32(sum_xor16(l_run[qb]));
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb) {
+    for (int qb = 0; qb < G::QB; ++qb) {
         const int qrow = qw + g::st16_query(lane, qb);
         if (qrow >= n) continue;
         const float inv = (l_tot[qb] > 0.0F) ? (1.0F / l_tot[qb]) : 0.0F;
         if (lse_h != nullptr && lane < 16) lse_h[qrow] = row_lse2(m_run[qb], l_tot[qb]) * kLn2;
-        f16* dst = oh + static_cast<size_t>(qrow) * 128 + 4 * (lane >> 4);
+        f16* dst = oh + static_cast<size_t>(qrow) * G::D + 4 * (lane >> 4);
 #pragma unroll
-        for (int db = 0; db < m16::DB; ++db) {
+        for (int db = 0; db < G::DB; ++db) {
             const f32x4& a = oacc[db][qb];
             *reinterpret_cast<f16x4*>(dst + 16 * db) =
                 pack4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
@@ -1523,47 +1617,47 @@ template <class T, bool CAUSAL>
 __device__ __forceinline__ void general_tiles16(
     int j, int n_tiles, int n_act, int n, int qw, int lane, const f16* kh, const f16* vh,
     char* const (&kb)[3], char* const (&vb)[3], const TileDma<T, true>& dma_k,
-    const TileDma<T>& dma, const Frag16& fr,
-    const f16x8 (&qf)[m16::QB][m16::DC], f32x4 (&s)[m16::KB][m16::QB],
-    f32x4 (&oacc)[m16::DB][m16::QB], float scale_log2, float (&m_run)[m16::QB],
-    float (&l_run)[m16::QB]) {
+    const TileDma<T>& dma, const Frag16<T>& fr, const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
+    f32x4 (&s)[M16<T>::KB][M16<T>::QB], f32x4 (&oacc)[M16<T>::DB][M16<T>::QB],
+    float scale_log2, float (&m_run)[M16<T>::QB], float (&l_run)[M16<T>::QB]) {
+    using G = M16<T>;
     for (; j < n_tiles; ++j) {
         wait_vmem();
         __syncthreads();
         const bool act = j < n_act;
         const bool act_next = j + 1 < n_act;
-        f16x8 kf[m16::KB][m16::DC];
-        f16x8 vf[m16::DB];
-        if (act_next) load_k16(kb[(j + 1) % 3], fr, kf);
-        if (act) load_v16(vb[j % 3], fr, vf);
+        f16x8 kf[G::KB][G::DC];
+        f16x8 vf[G::KS][G::DB];
+        if (act_next) load_k16<T>(kb[(j + 1) % 3], fr, kf);
+        if (act) load_v16<T>(vb[j % 3], fr, vf);
         if (j + 2 < n_tiles) load_tile<T>(kh, (j + 2) * T::BC, n, kb[(j + 2) % 3], dma_k);
         if (j + 1 < n_tiles) load_tile<T>(vh, (j + 1) * T::BC, n, vb[(j + 1) % 3], dma);
         if (!act) continue;  // wave-uniform: fully masked for this wave (causal)
-        f32x4 s2[m16::KB][m16::QB];
+        f32x4 s2[G::KB][G::QB];
         if (act_next) {
 #pragma unroll
-            for (int b = 0; b < m16::KB; ++b)
+            for (int b = 0; b < G::KB; ++b)
 #pragma unroll
-                for (int qb = 0; qb < m16::QB; ++qb) {
+                for (int qb = 0; qb < G::QB; ++qb) {
                     s2[b][qb] = f32x4{};
 #pragma unroll
-                    for (int dc = 0; dc < m16::DC; ++dc)
+                    for (int dc = 0; dc < G::DC; ++dc)
                         s2[b][qb] = mfma16(kf[b][dc], qf[qb][dc], s2[b][qb]);
                 }
         }
         const int kt = j * T::BC;
-        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask16<CAUSAL>(s, kt, n, qw, lane);
-        f16x8 p[m16::QB];
-        float alpha[m16::QB];
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask16<T, CAUSAL>(s, kt, n, qw, lane);
+        f16x8 p[G::QB][G::KS];
+        float alpha[G::QB];
         bool rescale;
         softmax16_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale16(oacc, alpha);
-        pv16(vf, p, oacc);
+        if (rescale) rescale16<T>(oacc, alpha);
+        pv16<T>(vf, p, oacc);
         if (act_next) {
 #pragma unroll
-            for (int b = 0; b < m16::KB; ++b)
+            for (int b = 0; b < G::KB; ++b)
 #pragma unroll
-                for (int qb = 0; qb < m16::QB; ++qb) s[b][qb] = s2[b][qb];
+                for (int qb = 0; qb < G::QB; ++qb) s[b][qb] = s2[b][qb];
         }
     }
 }
@@ -1574,7 +1668,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
     float* /*lse_part*/) {
-    static_assert(T::D == 128 && T::BC == 32, "the 16x16x32 layout is written for D=128, BC=32");
+    static_assert((T::D == 128 && T::BC == 32) || (T::D == 64 && T::BC == 64),
+                  "the 16x16x32 layouts are written for D=128, BC=32 and D=64, BC=64");
+    using G = M16<T>;
     static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
@@ -1619,26 +1715,26 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     load_tile<T>(kh, T::BC, n, kbuf(I1{}), dma_k);
     load_tile<T>(kh, 2 * T::BC, n, kbuf(I2{}), dma_k);
     load_tile<T>(vh, T::BC, n, vbuf(I1{}), dma);
-    f16x8 qf[m16::QB][m16::DC];
-    load_q16(q + head, qw, n, lane, negate_q, qf);
-    const Frag16 fr(lane);
+    f16x8 qf[G::QB][G::DC];
+    load_q16<T>(q + head, qw, n, lane, negate_q, qf);
+    const Frag16<T> fr(lane);
 
-    f32x4 oacc[m16::DB][m16::QB];
+    f32x4 oacc[G::DB][G::QB];
 #pragma unroll
-    for (int db = 0; db < m16::DB; ++db)
+    for (int db = 0; db < G::DB; ++db)
 #pragma unroll
-        for (int qb = 0; qb < m16::QB; ++qb) oacc[db][qb] = f32x4{};
-    float m_run[m16::QB] = {-INFINITY, -INFINITY};
-    float l_run[m16::QB] = {0.0F, 0.0F};
+        for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = f32x4{};
+    float m_run[G::QB] = {-INFINITY, -INFINITY};
+    float l_run[G::QB] = {0.0F, 0.0F};
 
     wait_vmem();
     __syncthreads();
 #pragma unroll
-    for (int qb = 0; qb < m16::QB; ++qb)
+    for (int qb = 0; qb < G::QB; ++qb)
 #pragma unroll
-        for (int dc = 0; dc < m16::DC; ++dc) asm volatile("" ::"v"(qf[qb][dc]));
-    f32x4 s[m16::KB][m16::QB];
-    if (n_act > 0) qk16(kbuf(I0{}), fr, qf, s);
+        for (int dc = 0; dc < G::DC; ++dc) asm volatile("" ::"v"(qf[qb][dc]));
+    f32x4 s[G::KB][G::QB];
+    if (n_act > 0) qk16<T>(kbuf(I0{}), fr, qf, s);
 
     FA_PHASE_DECL();
     auto steady = [&](auto group) {
@@ -1660,29 +1756,29 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             using Rj2 = std::integral_constant<int, (R + 2) % 3>;
             // softmax phase S_jj
             if (g::tile_needs_mask(n, jj * T::BC, T::BC, qw, CAUSAL)) {
-                mask16<CAUSAL>(s, jj * T::BC, n, qw, lane);
+                mask16<T, CAUSAL>(s, jj * T::BC, n, qw, lane);
             }
-            f16x8 kf[m16::KB][m16::DC];
-            f16x8 vf[m16::DB];
-            load_k16(kbuf(Rj1{}), fr, kf);
-            load_v16(vbuf(Rj{}), fr, vf);
-            f16x8 p[m16::QB];
+            f16x8 kf[G::KB][G::DC];
+            f16x8 vf[G::KS][G::DB];
+            load_k16<T>(kbuf(Rj1{}), fr, kf);
+            load_v16<T>(vbuf(Rj{}), fr, vf);
+            f16x8 p[G::QB][G::KS];
             bool overflow;
-            softmax16_optimistic(s, scale_log2, m_run, l_run, overflow, p);
-            static_assert(24 % FA_PP16_READS_PER == 0, "FA_PP16_READS_PER must divide 24");
-            sched_reads_valu<FA_PP16_READS_PER, FA_PP16_VALU_PER, 24 / FA_PP16_READS_PER>();
+            softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
+            static_assert(G::READS % FA_PP16_READS_PER == 0, "FA_PP16_READS_PER must divide 24");
+            sched_reads_valu<FA_PP16_READS_PER, FA_PP16_VALU_PER, G::READS / FA_PP16_READS_PER>();
             FA_PHASE_T(tb);
             end_phase<G == 1>();
             FA_PHASE_T(tc);
             // matrix phase M_jj
             if (__builtin_expect(overflow, 0)) {
-                float alpha[m16::QB];
+                float alpha[G::QB];
                 bool rescale;
                 softmax16_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-                if (rescale) rescale16(oacc, alpha);
+                if (rescale) rescale16<T>(oacc, alpha);
             }
             __builtin_amdgcn_s_setprio(FA_PP_PRIO);
-            matrix_phase16(kf, qf, vf, p, s, oacc, [&] {
+            matrix_phase16<T>(kf, qf, vf, p, s, oacc, [&] {
                 if constexpr (G == 0) {
                     refill(jj + 3, Rj{}, jj + 2, Rj2{});
                 } else {
@@ -1722,8 +1818,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     vb[2] = v_lds2;
     general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, n, qw, lane, kh, vh, kb, vb, dma_k, dma,
                                fr, qf, s, oacc, scale_log2, m_run, l_run);
-    store16(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane, m_run,
-            l_run, oacc);
+    store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane, m_run,
+               l_run, oacc);
     FA_PHASE_STORE(wave, lane);
     FA_CLOCK_END();
 }
@@ -1757,7 +1853,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #define FA_OPT_D64_SHORT 64, 8, true, SIMPLE
 #endif
 #ifndef FA_OPT_D64
-#define FA_OPT_D64 64, 8, true, PINGPONG
+#define FA_OPT_D64 64, 8, true, PINGPONG16
 #endif
 #ifndef FA_OPT_D64_CAUSAL_SHORT
 #define FA_OPT_D64_CAUSAL_SHORT 64, 8, true, SIMPLE
@@ -1766,7 +1862,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #define FA_OPT_D64_CAUSAL 32, 4, true, PIPE
 #endif
 #ifndef FA_OPT_D64_CAUSAL_LONG
-#define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG
+#define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG16
 #endif
 #ifndef FA_OPT_D128
 #define FA_OPT_D128 32, 8, true, PINGPONG16

@@ -12,8 +12,8 @@ slot: one row of the tile table in csrc/flash_fwd.hip, named after its macro (se
       opt_d128_causal_short, opt_d128_causal, base_d64, base_d128
 cand: "BC,NW,LAZY,SCHED" -- keys per tile, query waves per workgroup (BR = 32 * NW), lazy
       rescale (true/false) and schedule (SIMPLE, PIPE, PINGPONG, KSPLIT, which runs two waves
-      per query wave, or PINGPONG16, the ping-pong on 16x16x32 MFMAs for D=128 with BC=32 and
-      8 waves), e.g. 32,8,true,PINGPONG16.
+      per query wave, or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128,
+      BC=64 at D=64), e.g. 32,8,true,PINGPONG16.
       Without candidates a default list for the slot is used.
 
 `build` compiles csrc/flash_fwd.hip once per candidate with the slot's macro overridden, into
@@ -72,7 +72,8 @@ SLOTS = {
     "base_d128": ("FA_BASE_D128", "base", 128, 0, []),
 }
 DEFAULT_CANDS = {
-    64: ["32,4,true,PIPE", "64,4,true,PIPE", "64,8,true,PINGPONG", "32,4,true,SIMPLE",
+    64: ["32,4,true,PIPE", "64,4,true,PIPE", "64,8,true,PINGPONG16", "64,8,true,PINGPONG",
+         "32,4,true,SIMPLE",
          "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "64,2,true,KSPLIT",
          "32,2,true,KSPLIT"],
     128: ["32,8,true,PINGPONG16", "32,8,true,PINGPONG", "32,8,true,PIPE", "32,4,true,SIMPLE",

@@ -18,15 +18,15 @@ int geom_tr16_row(int lane) { return g::tr16_row(lane); }
 int geom_tr16_col(int lane) { return g::tr16_col(lane); }
 int geom_st_key(int lane, int nb, int r) { return g::st_key(lane, nb, r); }
 int geom_m16_key(int kb, int i) { return g::m16_key(kb, i); }
-int geom_m16_kchunk(int dc, int grp) { return g::m16_kchunk(dc, grp); }
-int geom_m16_kslot_row(int slot) { return g::m16_kslot_row(slot); }
-int geom_m16_kslot_chunk(int slot) { return g::m16_kslot_chunk(slot); }
-int geom_row_xor_m16(int row) { return g::row_xor_m16(row); }
-int geom_swizzle_chunk_m16(int row, int chunk) { return g::swizzle_chunk_m16(row, chunk); }
-int geom_tile_offset_m16(int row, int chunk) { return g::tile_offset_m16(row, chunk); }
+int geom_m16_kchunk(int dc, int grp, int d) { return g::m16_kchunk(dc, grp, d); }
+int geom_m16_kslot_row(int slot, int d) { return g::m16_kslot_row(slot, d); }
+int geom_m16_kslot_chunk(int slot, int d) { return g::m16_kslot_chunk(slot, d); }
+int geom_row_xor_m16(int row, int d) { return g::row_xor_m16(row, d); }
+int geom_swizzle_chunk_m16(int row, int chunk, int d) { return g::swizzle_chunk_m16(row, chunk, d); }
+int geom_tile_offset_m16(int row, int chunk, int d) { return g::tile_offset_m16(row, chunk, d); }
 int geom_st16_key(int lane, int kb, int r) { return g::st16_key(lane, kb, r); }
 int geom_st16_query(int lane, int qb) { return g::st16_query(lane, qb); }
-int geom_pv16_key(int lane, int i) { return g::pv16_key(lane, i); }
+int geom_pv16_key(int lane, int t, int i) { return g::pv16_key(lane, t, i); }
 int geom_pv_key(int lane, int i) { return g::pv_key(lane, i); }
 int geom_num_kv_tiles(int n, int q0, int block_q, int block_k, int causal) {
     return g::num_kv_tiles(n, q0, block_q, block_k, causal != 0);

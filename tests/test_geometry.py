@@ -169,122 +169,148 @@ def test_p_operand_slots_are_the_score_accumulators(geo):
         assert geo.geom_st_key(lane, nb, 8 * h + i) == 32 * nb + 16 * h + geo.geom_pv_key(lane, i)
 
 
-# ---- the 16x16x32 layout (flash_fwd_pingpong16, D = 128) ----------------------------------
+# ---- the 16x16x32 layout (flash_fwd_pingpong16: d = 128 with 32-key tiles, d = 64 with 64) --
+
+M16 = {128: dict(bc=32, kb=2, dc=4, db=8, ks=1), 64: dict(bc=64, kb=4, dc=2, db=4, ks=2)}
+
 
 def test_m16_key_blocks_split_the_tile(geo):
-    """Key block kb holds rows 8kb + {0..7, 16..23}: its 16 rows cover both 4 KiB halves."""
-    for kb in range(2):
+    """Key block kb holds rows 32(kb/2) + 8(kb%2) + {0..7, 16..23}: its 16 rows lie in both
+    16-row halves of its 32-key group."""
+    for kb in range(4):
+        base = 32 * (kb // 2) + 8 * (kb % 2)
         rows = [geo.geom_m16_key(kb, i) for i in range(16)]
-        assert rows == [8 * kb + r for r in range(8)] + [8 * kb + 16 + r for r in range(8)]
-    assert sorted(geo.geom_m16_key(kb, i) for kb in range(2) for i in range(16)) == list(range(32))
+        assert rows == [base + r for r in range(8)] + [base + 16 + r for r in range(8)]
+    for d, c in M16.items():
+        assert sorted(geo.geom_m16_key(kb, i) for kb in range(c["kb"]) for i in range(16)) == \
+            list(range(c["bc"]))
 
 
-def test_m16_swizzle_is_a_permutation_of_each_row(geo):
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_swizzle_is_a_permutation_of_each_row(geo, d):
+    cpr = d // 8
     for row in range(256):
-        phys = [geo.geom_swizzle_chunk_m16(row, c) for c in range(16)]
-        assert sorted(phys) == list(range(16))
-        assert all(geo.geom_swizzle_chunk_m16(row, p) == c for c, p in enumerate(phys))
-        assert geo.geom_row_xor_m16(row) == geo.geom_row_xor_m16(row % 32)
-    for row in list(range(8)) + list(range(16, 24)):  # +8 rows (kb = 1) keeps the xor
-        assert geo.geom_row_xor_m16(row + 8) == geo.geom_row_xor_m16(row)
+        phys = [geo.geom_swizzle_chunk_m16(row, c, d) for c in range(cpr)]
+        assert sorted(phys) == list(range(cpr))
+        assert all(geo.geom_swizzle_chunk_m16(row, p, d) == c for c, p in enumerate(phys))
+        # +8 rows inside a key block's half, and +32 rows (next key group), keep the xor
+        assert geo.geom_row_xor_m16(row + 32, d) == geo.geom_row_xor_m16(row, d)
+        if row % 16 < 8:
+            assert geo.geom_row_xor_m16(row + 8, d) == geo.geom_row_xor_m16(row, d)
 
 
-def test_m16_k_tile_layout_is_a_permutation(geo):
-    cells = [(geo.geom_m16_kslot_row(s), geo.geom_m16_kslot_chunk(s)) for s in range(512)]
-    assert sorted(cells) == [(r, c) for r in range(32) for c in range(16)]
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_k_tile_layout_is_a_permutation(geo, d):
+    bc, cpr = M16[d]["bc"], d // 8
+    cells = [(geo.geom_m16_kslot_row(s, d), geo.geom_m16_kslot_chunk(s, d)) for s in range(bc * cpr)]
+    assert sorted(cells) == [(r, c) for r in range(bc) for c in range(cpr)]
 
 
-def test_m16_k_reads_use_the_32x32_addresses_and_get_the_operand(geo):
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_k_reads_use_the_32x32_addresses_and_get_the_operand(geo, d):
     """The K operand of MFMA step (kb, dc) is read at the 32x32x16 path's fragment addresses
-    for kk = 4kb + dc (conflict-free, test_k_fragment_reads_are_conflict_free), and lane l gets
-    key row m16_key(kb, l%16), chunk m16_kchunk(dc, l//16); the chunks of the four lane groups
-    of one step are four different 16-byte pieces of the row."""
-    for kb, dc in itertools.product(range(2), range(4)):
-        offs = _k_offsets(geo, 128, 0, 4 * kb + dc)
+    (nb = kb/2, kk = (kb%2)*DC + dc; conflict-free, test_k_fragment_reads_are_conflict_free),
+    and lane l gets key row m16_key(kb, l%16), chunk m16_kchunk(dc, l//16)."""
+    c = M16[d]
+    for kb, dc in itertools.product(range(c["kb"]), range(c["dc"])):
+        offs = _k_offsets(geo, d, kb // 2, (kb % 2) * c["dc"] + dc)
         for l, o in enumerate(offs):
             assert o % 16 == 0
             slot = o // 16
-            assert geo.geom_m16_kslot_row(slot) == geo.geom_m16_key(kb, l % 16), (kb, dc, l)
-            assert geo.geom_m16_kslot_chunk(slot) == geo.geom_m16_kchunk(dc, l // 16), (kb, dc, l)
-    # the Q^T operand order: features 8*m16_kchunk(dc, g) .. +7 cover D = 128 once per lane group
-    assert sorted(geo.geom_m16_kchunk(dc, g) for dc in range(4) for g in range(4)) == list(range(16))
+            assert geo.geom_m16_kslot_row(slot, d) == geo.geom_m16_key(kb, l % 16), (kb, dc, l)
+            assert geo.geom_m16_kslot_chunk(slot, d) == geo.geom_m16_kchunk(dc, l // 16, d)
+    # the Q^T operand order: features 8*m16_kchunk(dc, g) .. +7 cover D once per lane
+    assert sorted(geo.geom_m16_kchunk(dc, g, d) for dc in range(c["dc"]) for g in range(4)) == \
+        list(range(d // 8))
 
 
-def test_m16_k_tile_dma_reads_whole_64_byte_pieces(geo):
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_k_tile_dma_reads_whole_64_byte_pieces(geo, d):
     """Each DMA request (64 consecutive LDS slots) reads its global chunks as aligned runs of
     four (64 bytes), so the permuted layout costs no extra global sectors."""
-    for s0 in range(0, 512, 64):
-        src = sorted(256 * geo.geom_m16_kslot_row(s) + 16 * geo.geom_m16_kslot_chunk(s)
+    rb, n = 2 * d, M16[d]["bc"] * d // 8
+    for s0 in range(0, n, 64):
+        src = sorted(rb * geo.geom_m16_kslot_row(s, d) + 16 * geo.geom_m16_kslot_chunk(s, d)
                      for s in range(s0, s0 + 64))
         pieces = {a // 64 for a in src}
         assert len(pieces) == 16, s0
         assert all(sum(1 for a in src if a // 64 == p) == 4 for p in pieces)
 
 
-def _v16_read_offsets(geo, db, e):
-    """V^T transposed read e (0, 1) of fragment db: lane l addresses row
-    pv16_key(l, 4e) + tr16_row(l), feature column 16*db + tr16_col(l)."""
+def _v16_read_offsets(geo, d, t, db, e):
+    """V^T transposed read e (0, 1) of k step t, fragment db: lane l addresses row
+    pv16_key(l, t, 4e) + tr16_row(l), feature column 16*db + tr16_col(l)."""
     out = []
     for l in range(64):
-        row = geo.geom_pv16_key(l, 4 * e) + geo.geom_tr16_row(l)
+        row = geo.geom_pv16_key(l, t, 4 * e) + geo.geom_tr16_row(l)
         colh = 16 * db + geo.geom_tr16_col(l)
-        out.append(geo.geom_tile_offset_m16(row, colh // 8) + 2 * (colh % 8))
-    if e == 1:  # the kernel reads it 8 rows after the first
-        first = _v16_read_offsets(geo, db, 0)
-        assert all(o == f + 8 * 256 for o, f in zip(out, first))
+        out.append(geo.geom_tile_offset_m16(row, colh // 8, d) + 2 * (colh % 8))
+    base = [geo.geom_tile_offset_m16(geo.geom_pv16_key(l, 0, 0) + geo.geom_tr16_row(l),
+                                     (16 * db + geo.geom_tr16_col(l)) // 8, d)
+            + 2 * ((16 * db + geo.geom_tr16_col(l)) % 8) for l in range(64)]
+    # the kernel reads it at the (t, e) = (0, 0) offset plus 32t + 8e rows (immediates)
+    assert all(o == b + (32 * t + 8 * e) * 2 * d for o, b in zip(out, base))
     return out
 
 
-def test_m16_v_transposed_reads_are_conflict_free(geo):
-    for db, e in itertools.product(range(8), range(2)):
-        offs = _v16_read_offsets(geo, db, e)
-        assert _conflict_free(offs, 8, 32), (db, e)
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_v_transposed_reads_are_conflict_free(geo, d):
+    c = M16[d]
+    for t, db, e in itertools.product(range(c["ks"]), range(c["db"]), range(2)):
+        offs = _v16_read_offsets(geo, d, t, db, e)
+        assert _conflict_free(offs, 8, 32), (t, db, e)
         for g0 in range(0, 64, 32):
             banks = sum((_banks(o, 8) for o in offs[g0:g0 + 32]), [])
-            assert sorted(banks) == list(range(64)), (db, e, g0)
+            assert sorted(banks) == list(range(64)), (t, db, e, g0)
 
 
-def test_m16_v_transposed_reads_deliver_the_pv16_keys(geo):
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_v_transposed_reads_deliver_the_pv16_keys(geo, d):
     """Each 16-lane group reads a 4-row x 16-column block whose transpose hands lane l feature
-    16*db + l%16 at keys pv16_key(l, 4e + i), i = 0..3."""
-    for db, e in itertools.product(range(8), range(2)):
-        offs = _v16_read_offsets(geo, db, e)
+    16*db + l%16 at keys pv16_key(l, t, 4e + i), i = 0..3."""
+    c, rb = M16[d], 2 * d
+    for t, db, e in itertools.product(range(c["ks"]), range(c["db"]), range(2)):
+        offs = _v16_read_offsets(geo, d, t, db, e)
         for g0 in range(0, 64, 16):
             cells = []
             for l in range(g0, g0 + 16):
-                row = offs[l] // 256
-                phys_chunk = (offs[l] % 256) // 16
-                colh = 8 * geo.geom_swizzle_chunk_m16(row, phys_chunk) + (offs[l] % 16) // 2
+                row = offs[l] // rb
+                phys_chunk = (offs[l] % rb) // 16
+                colh = 8 * geo.geom_swizzle_chunk_m16(row, phys_chunk, d) + (offs[l] % 16) // 2
                 cells.append((row, colh))
             rows = sorted({r for r, _ in cells})
             assert len(rows) == 4 and rows == list(range(rows[0], rows[0] + 4))
-            cols = sorted({c + j for _, c in cells for j in range(4)})
+            cols = sorted({col + j for _, col in cells for j in range(4)})
             assert cols == list(range(cols[0], cols[0] + 16))
             for j in range(16):
                 lane = g0 + j
                 assert cols[0] + j == 16 * db + lane % 16
                 for i in range(4):
-                    assert rows[i] == geo.geom_pv16_key(lane, 4 * e + i)
+                    assert rows[i] == geo.geom_pv16_key(lane, t, 4 * e + i)
 
 
-def test_m16_p_operand_slots_are_the_score_accumulators(geo):
-    """Slot 4*kb + r of the P^T operand is score accumulator r of block kb, and the key of a
-    slot depends only on lane // 16 (the MFMA pairs A and B slots by k index, 8*(lane//16)+i)."""
-    for lane, kb, r in itertools.product(range(64), range(2), range(4)):
-        assert geo.geom_st16_key(lane, kb, r) == geo.geom_pv16_key(lane, 4 * kb + r)
-    for lane, i in itertools.product(range(64), range(8)):
-        assert geo.geom_pv16_key(lane, i) == geo.geom_pv16_key(16 * (lane // 16), i)
-    # the 32 k indices of one MFMA cover the 32 keys of the tile once
-    keys = {geo.geom_pv16_key(16 * g, i) for g in range(4) for i in range(8)}
-    assert keys == set(range(32))
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_p_operand_slots_are_the_score_accumulators(geo, d):
+    """Slot 4*(kb%2) + r of k step kb//2 of the P^T operand is score accumulator r of block kb,
+    and the key of a slot depends only on lane // 16 (the MFMA pairs A and B slots by k index,
+    8*(lane//16) + i); the 32 k indices of a step cover its 32 keys once."""
+    c = M16[d]
+    for lane, kb, r in itertools.product(range(64), range(c["kb"]), range(4)):
+        assert geo.geom_st16_key(lane, kb, r) == geo.geom_pv16_key(lane, kb // 2, 4 * (kb % 2) + r)
+    for lane, t, i in itertools.product(range(64), range(c["ks"]), range(8)):
+        assert geo.geom_pv16_key(lane, t, i) == geo.geom_pv16_key(16 * (lane // 16), t, i)
+    for t in range(c["ks"]):
+        keys = {geo.geom_pv16_key(16 * g, t, i) for g in range(4) for i in range(8)}
+        assert keys == set(range(32 * t, 32 * t + 32))
 
 
-def test_m16_score_blocks_cover_the_tile_once(geo):
+@pytest.mark.parametrize("d", [64, 128])
+def test_m16_score_blocks_cover_the_tile_once(geo, d):
+    c = M16[d]
     cells = {(geo.geom_st16_key(l, kb, r), geo.geom_st16_query(l, qb))
-             for l in range(64) for kb in range(2) for qb in range(2) for r in range(4)}
-    assert cells == {(k, q) for k in range(32) for q in range(32)}
-    # and the K operand rows (M index lane%16 of block kb) are the keys the scores carry
-    for lane, kb, r in itertools.product(range(64), range(2), range(4)):
+             for l in range(64) for kb in range(c["kb"]) for qb in range(2) for r in range(4)}
+    assert cells == {(k, q) for k in range(c["bc"]) for q in range(32)}
+    for lane, kb, r in itertools.product(range(64), range(c["kb"]), range(4)):
         assert geo.geom_st16_key(lane, kb, r) == geo.geom_m16_key(kb, geo.geom_mfma16_c_row(lane, r))
 
 
