@@ -122,8 +122,9 @@ namespace g = fa::geom;
 // groups of waves alternate between an MFMA-only phase and a softmax phase), KSPLIT
 // (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles), PINGPONG16
 // (flash_fwd_pingpong16: the ping-pong schedule on 16x16x32 MFMAs; the table's long-sequence
-// rows; PINGPONG stays for A/B builds).
-enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3, PINGPONG16 = 4 };
+// rows; PINGPONG stays for A/B builds), SIMPLE16 (flash_fwd_simple16: the simple schedule on
+// 16x16x32 MFMAs).
+enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3, PINGPONG16 = 4, SIMPLE16 = 5 };
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
@@ -138,8 +139,8 @@ struct Tile {
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
-    static constexpr bool M16 = SCHED == PINGPONG16;   // 16x16x32 MFMA layout and swizzle
-    static constexpr int NBUF = (SCHED == PINGPONG || M16) ? 3 : 2;  // buffers each for K, V
+    static constexpr bool M16 = SCHED == PINGPONG16 || SCHED == SIMPLE16;  // 16x16x32 layouts
+    static constexpr int NBUF = (SCHED == PINGPONG || SCHED == PINGPONG16) ? 3 : 2;  // per K, V
     static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES * KS;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
@@ -1824,6 +1825,112 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     FA_CLOCK_END();
 }
 
+// ---- simple schedule on 16x16x32 MFMAs ---------------------------------------------------------
+// flash_fwd_kernel's schedule (barrier, prefetch of tile j+1, QK^T, exact softmax and P.V of tile
+// j) with the 16x16x32 layouts of flash_fwd_pingpong16. Fragments are read from LDS right before
+// the MFMAs that use them, so that the d=64 tile keeps four waves per SIMD.
+template <class T>
+__device__ __forceinline__ void qk16_inline(const char* kl, const Frag16<T>& fr,
+                                            const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
+                                            f32x4 (&s)[M16<T>::KB][M16<T>::QB]) {
+    using G = M16<T>;
+#pragma unroll
+    for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = f32x4{};
+#pragma unroll
+    for (int dc = 0; dc < G::DC; ++dc)
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb) {
+            const f16x8 a = *reinterpret_cast<const f16x8*>(kl + fr.koff[kb][dc]);
+#pragma unroll
+            for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = mfma16(a, qf[qb][dc], s[kb][qb]);
+        }
+}
+
+template <class T>
+__device__ __forceinline__ void pv16_inline(const char* vl, const Frag16<T>& fr,
+                                            const f16x8 (&p)[M16<T>::QB][M16<T>::KS],
+                                            f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
+    using G = M16<T>;
+#pragma unroll
+    for (int t = 0; t < G::KS; ++t)
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+            const char* base = vl + fr.voff[db] + 32 * t * G::ROW;
+            const f16x4 lo = lds_read_tr16(base);
+            const f16x4 up = lds_read_tr16(base + 8 * G::ROW);
+            const f16x8 a = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+#pragma unroll
+            for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = mfma16(a, p[qb][t], oacc[db][qb]);
+        }
+}
+
+template <class T, bool CAUSAL>
+__global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
+    float* /*lse_part*/) {
+    using G = M16<T>;
+    static_assert(T::NBUF == 2, "double-buffered K and V");
+    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+    FA_CLOCK_BEGIN();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_uniform(threadIdx.x >> 6);
+    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
+    const f16* kh = k + head;
+    const f16* vh = v + head;
+    const int q0 = w.qb * T::BR;
+    const int qw = q0 + wave * 32;  // first query of this wave
+    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+
+    // LDS: [K0 | K1 | V0 | V1]; buffer b of K at b*TILE_BYTES, of V at (2+b)*TILE_BYTES.
+    auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
+    auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
+
+    const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
+    const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
+    load_tile<T>(kh, 0, n, kbuf(0), dma_k);
+    load_tile<T>(vh, 0, n, vbuf(0), dma);
+    f16x8 qf[G::QB][G::DC];
+    load_q16<T>(q + head, qw, n, lane, negate_q, qf);
+    const Frag16<T> fr(lane);
+
+    f32x4 oacc[G::DB][G::QB];
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = f32x4{};
+    float m_run[G::QB] = {-INFINITY, -INFINITY};
+    float l_run[G::QB] = {0.0F, 0.0F};
+
+    for (int j = 0; j < n_tiles; ++j) {
+        wait_vmem();
+        __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
+        if (j + 1 < n_tiles) {
+            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf((j + 1) & 1), dma_k);
+            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), dma);
+        }
+        const int kt = j * T::BC;
+        if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) continue;  // wave-uniform
+        f32x4 s[G::KB][G::QB];
+        qk16_inline<T>(kbuf(j & 1), fr, qf, s);
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask16<T, CAUSAL>(s, kt, n, qw, lane);
+        f16x8 p[G::QB][G::KS];
+        float alpha[G::QB];
+        bool rescale;
+        softmax16_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale16<T>(oacc, alpha);
+        pv16_inline<T>(vbuf(j & 1), fr, p, oacc);
+    }
+    store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane, m_run,
+               l_run, oacc);
+    FA_CLOCK_END();
+}
+
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
 // (csrc/kernels/flash_fwd.cu:597-612). On MI355X the best tile also depends on the sequence
@@ -2018,6 +2125,8 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
     } else if constexpr (T::SCHED == PINGPONG16) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL>);
+    } else if constexpr (T::SCHED == SIMPLE16) {
+        fn = reinterpret_cast<const void*>(&flash_fwd_simple16<T, CAUSAL>);
     } else if constexpr (T::SCHED == KSPLIT) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
     } else if constexpr (T::SCHED == PIPE) {

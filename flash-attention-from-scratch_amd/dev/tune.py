@@ -13,7 +13,7 @@ slot: one row of the tile table in csrc/flash_fwd.hip, named after its macro (se
 cand: "BC,NW,LAZY,SCHED" -- keys per tile, query waves per workgroup (BR = 32 * NW), lazy
       rescale (true/false) and schedule (SIMPLE, PIPE, PINGPONG, KSPLIT, which runs two waves
       per query wave, or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128,
-      BC=64 at D=64), e.g. 32,8,true,PINGPONG16.
+      BC=64 at D=64; SIMPLE16 the simple schedule on those layouts), e.g. 32,8,true,PINGPONG16.
       Without candidates a default list for the slot is used.
 
 `build` compiles csrc/flash_fwd.hip once per candidate with the slot's macro overridden, into
@@ -73,10 +73,11 @@ SLOTS = {
 }
 DEFAULT_CANDS = {
     64: ["32,4,true,PIPE", "64,4,true,PIPE", "64,8,true,PINGPONG16", "64,8,true,PINGPONG",
-         "32,4,true,SIMPLE",
+         "32,4,true,SIMPLE", "64,8,true,SIMPLE16",
          "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "64,2,true,KSPLIT",
          "32,2,true,KSPLIT"],
     128: ["32,8,true,PINGPONG16", "32,8,true,PINGPONG", "32,8,true,PIPE", "32,4,true,SIMPLE",
+          "32,4,true,SIMPLE16",
           "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "32,2,true,KSPLIT",
           "32,4,true,KSPLIT"],
 }
