@@ -1308,6 +1308,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 #ifndef FA_PP16_VALU_PER
 #define FA_PP16_VALU_PER 16
 #endif
+// Matrix phase: the refill goes after MFMA pair FA_PP16_MID; FA_PP16_PV_FIRST puts each pair's
+// P.V MFMA before its QK^T one.
+#ifndef FA_PP16_MID
+#define FA_PP16_MID 1
+#endif
+#ifndef FA_PP16_PV_FIRST
+#define FA_PP16_PV_FIRST 0
+#endif
 // Per-tile geometry of the 16x16x32 path: D = 128 with 32-key tiles or D = 64 with 64-key
 // tiles; either way 32 MFMAs of each kind per wave and tile and 24 fragment reads.
 template <class T>
@@ -1550,8 +1558,8 @@ __device__ __forceinline__ void pv16(const f16x8 (&vf)[M16<T>::KS][M16<T>::DB],
 }
 
 // Matrix phase: S^T_{j+1} (16 MFMAs: KB*QB independent chains of DC, step i on chain i % (KB*QB))
-// alternating with O^T += V_j^T P_j^T (16 MFMAs, independent); `mid` (the refill) after the
-// first 8.
+// alternating with O^T += V_j^T P_j^T (16 MFMAs, independent); `mid` (the refill) after pair
+// FA_PP16_MID (the second pair: measured best of pairs 0-3 and 7, by about 1 %).
 template <class T, class Mid>
 __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16<T>::DC],
                                                const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
@@ -1572,13 +1580,18 @@ __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16
         const int kb = ch / G::QB;
         const int qs = ch % G::QB;
         const int dc = i / NCH;
-        s[kb][qs] = mfma16(kf[kb][dc], qf[qs][dc], s[kb][qs]);
         const int qv = i % G::QB;
         const int db = (i / G::QB) % G::DB;
         const int t = i / (G::QB * G::DB);
-        oacc[db][qv] = mfma16(vf[t][db], p[qv][t], oacc[db][qv]);
+        if (FA_PP16_PV_FIRST) {
+            oacc[db][qv] = mfma16(vf[t][db], p[qv][t], oacc[db][qv]);
+            s[kb][qs] = mfma16(kf[kb][dc], qf[qs][dc], s[kb][qs]);
+        } else {
+            s[kb][qs] = mfma16(kf[kb][dc], qf[qs][dc], s[kb][qs]);
+            oacc[db][qv] = mfma16(vf[t][db], p[qv][t], oacc[db][qv]);
+        }
         __builtin_amdgcn_sched_barrier(0);  // keep the alternation
-        if (i == 3) {
+        if (i == FA_PP16_MID) {
             mid();
             __builtin_amdgcn_sched_barrier(0);
         }
