@@ -21,6 +21,10 @@
 //     converted to fp16 in place and never moves. V^T comes from LDS through the gfx950
 //     transposing read ds_read_b64_tr_b16, which hands each lane 4 consecutive keys of one
 //     feature column.
+//   * The long-sequence rows (flash_fwd_pingpong16) do the same work on v_mfma_f32_16x16x32_f16,
+//     two MFMAs per 32x32x16 one: at MI355X's power limit that shape sustains about 20 % more
+//     FLOPS. Each lane then holds 4 keys of two queries per 16-key block; row statistics span the
+//     four lanes of a query (v_permlane16_swap and v_permlane32_swap).
 //   * Causal: tiles right of the diagonal are never loaded; masking runs only on diagonal and
 //     tail tiles; longest query blocks launch first.
 //   * Ragged N: the buffer resource of a K/V tile ends at row N, so rows >= N arrive as zeros
