@@ -2007,7 +2007,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
 #define FA_D64_CAUSAL_MAX_N 8192
 #endif
 #ifndef FA_D128_CAUSAL_SHORT_MAX_N
-#define FA_D128_CAUSAL_SHORT_MAX_N 3072
+#define FA_D128_CAUSAL_SHORT_MAX_N 2048
 #endif
 #ifndef FA_SMALL_GRID_WGS
 #define FA_SMALL_GRID_WGS 256

@@ -129,8 +129,8 @@ def test_tile_config_rows():
     assert _tile(64, True, "opt", 8192) == (128, 32, 4, 16384)
     assert _tile(64, True, "opt", 8193) == pingpong64
     assert _tile(128, False, "opt", 512) == (256, 32, 8, 49152)        # ping-pong at every N
-    assert _tile(128, True, "opt", 3072) == (128, 32, 4, 32768)        # simple, 4 waves
-    assert _tile(128, True, "opt", 3073) == (256, 32, 8, 49152)
+    assert _tile(128, True, "opt", 2048) == (128, 32, 4, 32768)        # simple, 4 waves
+    assert _tile(128, True, "opt", 2049) == (256, 32, 8, 49152)
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
     # two waves on each 32 rows)
     assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 4, 65536)

@@ -75,7 +75,7 @@ SWITCHES = [
     (1, 32, 2048, 64, False, SIMPLE64X8), (1, 32, 2049, 64, False, PP64),
     (1, 16, 4096, 64, True, SIMPLE64X8), (1, 16, 4097, 64, True, PIPE64),
     (1, 8, 8192, 64, True, PIPE64), (1, 8, 8193, 64, True, PP64),
-    (1, 24, 3072, 128, True, SIMPLE128X4), (1, 24, 3073, 128, True, PP128),
+    (1, 32, 2048, 128, True, SIMPLE128X4), (1, 32, 2049, 128, True, PP128),
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
 ]
