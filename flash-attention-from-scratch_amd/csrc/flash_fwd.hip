@@ -1712,7 +1712,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
     const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
     // Every tile but the last runs in the steady phases (diagonal and tail tiles masked there).
+    // A causal wave computes the first n_busy of them; the non-causal kernel computes all (a
+    // wave past the end of the sequence works on masked scores there), which keeps its steady
+    // loop free of the idle-tile code.
     const int n_steady = max(0, n_tiles - 1);
+    const int n_busy = CAUSAL ? min(n_steady, n_act) : n_steady;
 
     auto kbuf = [&](auto b) {
         constexpr int B = decltype(b)::value;
@@ -1810,13 +1814,32 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             FA_PHASE_TILE(ta, tb, tc, td, te);
         };
         int jj = 0;
-        for (; jj + 3 <= n_steady; jj += 3) {
+        for (; jj + 3 <= n_busy; jj += 3) {
             tile(jj, I0{});
             tile(jj + 1, I1{});
             tile(jj + 2, I2{});
         }
-        if (jj < n_steady) tile(jj, I0{});
-        if (jj + 1 < n_steady) tile(jj + 1, I1{});
+        if (jj < n_busy) tile(jj, I0{});
+        if (jj + 1 < n_busy) tile(jj + 1, I1{});
+        // Causal steady tiles whose keys are all masked for this wave (diagonal block, or a wave
+        // past the end of the sequence): the wave keeps only its two barriers per tile and its
+        // share of the refill DMA, in the order of a busy tile.
+        if constexpr (CAUSAL) {
+            auto kb_at = [&](int b) { return b == 0 ? k_lds0 : (b == 1 ? k_lds1 : k_lds2); };
+            auto vb_at = [&](int b) { return b == 0 ? v_lds0 : (b == 1 ? v_lds1 : v_lds2); };
+            for (int t = n_busy; t < n_steady; ++t) {
+                const int r = t % 3;
+                end_phase<G == 1>();
+                if constexpr (G == 0) {
+                    load_tile<T>(kh, (t + 3) * T::BC, n, kb_at(r), dma_k);
+                    load_tile<T>(vh, (t + 2) * T::BC, n, vb_at((r + 2) % 3), dma);
+                } else {
+                    load_tile<T>(kh, (t + 4) * T::BC, n, kb_at((r + 1) % 3), dma_k);
+                    load_tile<T>(vh, (t + 3) * T::BC, n, vb_at(r), dma);
+                }
+                end_phase<G == 0>();
+            }
+        }
         if constexpr (G == 0) end_phase<false>();
     };
     if (n_steady > 0) {
