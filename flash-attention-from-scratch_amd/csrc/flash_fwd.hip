@@ -1629,6 +1629,35 @@ __device__ __forceinline__ void store16(f16* oh, float* lse_h, int qw, int n, in
     }
 }
 
+// Split-KV partial of store16: O / l in fp32 and the base-2 LSE (scaled units) of the lane's two
+// queries (if < n), at op[qrow][d] and lp[qrow]; a row with no unmasked key in the range gets
+// O = 0 and LSE = -inf, which the combine kernel weighs 0. Same layout as the simple kernel's
+// store_partial.
+template <class T>
+__device__ __forceinline__ void store16_partial(float* op, float* lp, int qw, int n, int lane,
+                                                const float (&m_run)[M16<T>::QB],
+                                                const float (&l_run)[M16<T>::QB],
+                                                const f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
+    using G = M16<T>;
+    float l_tot[G::QB];
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) l_tot[qb] = sum_xor32(sum_xor16(l_run[qb]));
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) {
+        const int qrow = qw + g::st16_query(lane, qb);
+        if (qrow >= n) continue;
+        const float inv = (l_tot[qb] > 0.0F) ? (1.0F / l_tot[qb]) : 0.0F;
+        if (lane < 16) lp[qrow] = row_lse2(m_run[qb], l_tot[qb]);
+        float* dst = op + static_cast<size_t>(qrow) * G::D + 4 * (lane >> 4);
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+            const f32x4& a = oacc[db][qb];
+            *reinterpret_cast<f32x4*>(dst + 16 * db) =
+                f32x4{a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv};
+        }
+    }
+}
+
 // Tiles j .. n_tiles-1 outside the steady phases (as general_tiles): one barrier each; K_t
 // and V_t in buffer t % 3; refills of K_{j+2} and V_{j+1}.
 template <class T, bool CAUSAL>
@@ -1680,12 +1709,12 @@ __device__ __forceinline__ void general_tiles16(
     }
 }
 
-template <class T, bool CAUSAL>
+template <class T, bool CAUSAL, bool SPLIT = false>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
-    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
-    float* /*lse_part*/) {
+    float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
+    float* __restrict__ lse_part) {
     static_assert((T::D == 128 && T::BC == 32) || (T::D == 64 && T::BC == 64),
                   "the 16x16x32 layouts are written for D=128, BC=32 and D=64, BC=64");
     using G = M16<T>;
@@ -1703,14 +1732,30 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int grp = wave >> 2;
-    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const int items = bh_count * n_qblocks;
+    const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
+    const g::Work w = SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                                         n_qblocks, CAUSAL)
+                            : g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
-    const f16* kh = k + head;
-    const f16* vh = v + head;
     const int q0 = w.qb * T::BR;
-    const int qw = q0 + wave * 32;
-    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-    const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
+    const int qw = q0 + wave * 32;  // first query of this wave (Q loads, O stores)
+    // Split-KV: the workgroup runs key tiles [j_begin, j_begin + tiles_per_split) of its query
+    // block as if the keys started at key0: K/V pointers, the sequence end nk and the query
+    // position qk used by the masks are all taken relative to key0.
+    const int n_all = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const int j_begin = SPLIT ? split * tiles_per_split : 0;
+    if (SPLIT && j_begin >= n_all) return;  // workgroup-uniform: empty range
+    const int key0 = j_begin * T::BC;
+    const int nk = n - key0;
+    const int qk = qw - key0;
+    const f16* kh = k + head + static_cast<size_t>(key0) * T::D;
+    const f16* vh = v + head + static_cast<size_t>(key0) * T::D;
+    const int n_tiles = SPLIT ? min(n_all - j_begin, tiles_per_split) : n_all;
+    // (a split can start right of all of this wave's queries: no active tile then)
+    const int n_act = (SPLIT && CAUSAL && qk + 31 < 0)
+                          ? 0
+                          : g::wave_active_tiles(nk, qk, 32, T::BC, n_tiles, CAUSAL);
     // Every tile but the last runs in the steady phases (diagonal and tail tiles masked there).
     // A causal wave computes the first n_busy of them; the non-causal kernel computes all (a
     // wave past the end of the sequence works on masked scores there), which keeps its steady
@@ -1732,11 +1777,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 
     const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
     const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
-    load_tile<T>(kh, 0, n, kbuf(I0{}), dma_k);
-    load_tile<T>(vh, 0, n, vbuf(I0{}), dma);
-    load_tile<T>(kh, T::BC, n, kbuf(I1{}), dma_k);
-    load_tile<T>(kh, 2 * T::BC, n, kbuf(I2{}), dma_k);
-    load_tile<T>(vh, T::BC, n, vbuf(I1{}), dma);
+    load_tile<T>(kh, 0, nk, kbuf(I0{}), dma_k);
+    load_tile<T>(vh, 0, nk, vbuf(I0{}), dma);
+    load_tile<T>(kh, T::BC, nk, kbuf(I1{}), dma_k);
+    load_tile<T>(kh, 2 * T::BC, nk, kbuf(I2{}), dma_k);
+    load_tile<T>(vh, T::BC, nk, vbuf(I1{}), dma);
     f16x8 qf[G::QB][G::DC];
     load_q16<T>(q + head, qw, n, lane, negate_q, qf);
     const Frag16<T> fr(lane);
@@ -1762,8 +1807,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     auto steady = [&](auto group) {
         constexpr int G = decltype(group)::value;
         auto refill = [&](int a, auto pa, int b, auto pb) {
-            load_tile<T>(kh, a * T::BC, n, kbuf(pa), dma_k);
-            load_tile<T>(vh, b * T::BC, n, vbuf(pb), dma);
+            load_tile<T>(kh, a * T::BC, nk, kbuf(pa), dma_k);
+            load_tile<T>(vh, b * T::BC, nk, vbuf(pb), dma);
         };
         end_phase<false>();
         if constexpr (G == 1) {
@@ -1777,8 +1822,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             using Rj1 = std::integral_constant<int, (R + 1) % 3>;
             using Rj2 = std::integral_constant<int, (R + 2) % 3>;
             // softmax phase S_jj
-            if (g::tile_needs_mask(n, jj * T::BC, T::BC, qw, CAUSAL)) {
-                mask16<T, CAUSAL>(s, jj * T::BC, n, qw, lane);
+            if (g::tile_needs_mask(nk, jj * T::BC, T::BC, qk, CAUSAL)) {
+                mask16<T, CAUSAL>(s, jj * T::BC, nk, qk, lane);
             }
             f16x8 kf[G::KB][G::DC];
             f16x8 vf[G::KS][G::DB];
@@ -1831,11 +1876,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 const int r = t % 3;
                 end_phase<G == 1>();
                 if constexpr (G == 0) {
-                    load_tile<T>(kh, (t + 3) * T::BC, n, kb_at(r), dma_k);
-                    load_tile<T>(vh, (t + 2) * T::BC, n, vb_at((r + 2) % 3), dma);
+                    load_tile<T>(kh, (t + 3) * T::BC, nk, kb_at(r), dma_k);
+                    load_tile<T>(vh, (t + 2) * T::BC, nk, vb_at((r + 2) % 3), dma);
                 } else {
-                    load_tile<T>(kh, (t + 4) * T::BC, n, kb_at((r + 1) % 3), dma_k);
-                    load_tile<T>(vh, (t + 3) * T::BC, n, vb_at(r), dma);
+                    load_tile<T>(kh, (t + 4) * T::BC, nk, kb_at((r + 1) % 3), dma_k);
+                    load_tile<T>(vh, (t + 3) * T::BC, nk, vb_at(r), dma);
                 }
                 end_phase<G == 0>();
             }
@@ -1857,10 +1902,16 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     vb[0] = v_lds0;
     vb[1] = v_lds1;
     vb[2] = v_lds2;
-    general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, n, qw, lane, kh, vh, kb, vb, dma_k, dma,
-                               fr, qf, s, oacc, scale_log2, m_run, l_run);
-    store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane, m_run,
-               l_run, oacc);
+    general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
+                               dma, fr, qf, s, oacc, scale_log2, m_run, l_run);
+    if constexpr (SPLIT) {
+        const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
+        store16_partial<T>(o_part + part * n * T::D, lse_part + part * n, qw, n, lane, m_run,
+                           l_run, oacc);
+    } else {
+        store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
+                   m_run, l_run, oacc);
+    }
     FA_PHASE_STORE(wave, lane);
     FA_CLOCK_END();
 }
@@ -2159,8 +2210,13 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
                     static_cast<unsigned>(n_splits));
     const void* fn;
     if constexpr (SPLIT) {
-        static_assert(T::SCHED == SIMPLE, "split-KV runs the simple schedule");
-        fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
+        static_assert(T::SCHED == SIMPLE || T::SCHED == PINGPONG16,
+                      "split-KV runs the simple or the 16x16x32 ping-pong schedule");
+        if constexpr (T::SCHED == PINGPONG16) {
+            fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL, true>);
+        } else {
+            fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
+        }
     } else if constexpr (T::SCHED == PINGPONG) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
     } else if constexpr (T::SCHED == PINGPONG16) {
@@ -2184,22 +2240,48 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U) == 0; }
 
 // ---- split-KV ---------------------------------------------------------------------------------
-// Tile of the split-KV partial pass (simple schedule; each workgroup runs a bounded key range,
-// so there is no long steady state for the pipelined schedules to win back their prologue).
+// Rows of the split-KV partial pass, by (d, causal): the tile, and the automatic plan's target
+// number of workgroups with work and minimum keys per range. The 16x16x32 ping-pong runs the
+// long rows' tile over each key range; it wants about one workgroup per CU when not causal.
+// Causal d=64 keeps the 4-wave simple tile, whose smaller workgroups balance the ragged causal
+// ranges better (measured on few-head long shapes against the other candidates of this table).
 #ifndef FA_SPLIT_D64
-#define FA_SPLIT_D64 64, 4, true, SIMPLE
+#define FA_SPLIT_D64 64, 8, true, PINGPONG16
+#endif
+#ifndef FA_SPLIT_D64_CAUSAL
+#define FA_SPLIT_D64_CAUSAL 64, 4, true, SIMPLE
 #endif
 #ifndef FA_SPLIT_D128
-#define FA_SPLIT_D128 64, 4, true, SIMPLE
+#define FA_SPLIT_D128 32, 8, true, PINGPONG16
 #endif
-#ifndef FA_SPLIT_TARGET_WGS
-#define FA_SPLIT_TARGET_WGS 1024  // non-empty partial workgroups the automatic plan aims for
+#ifndef FA_SPLIT_D128_CAUSAL
+#define FA_SPLIT_D128_CAUSAL 32, 8, true, PINGPONG16
 #endif
-#ifndef FA_SPLIT_MIN_TILES
-#define FA_SPLIT_MIN_TILES 4  // key tiles per split at least
+#ifndef FA_SPLIT_PLAN
+#define FA_SPLIT_PLAN 256, 512  // non-causal: target workgroups, minimum keys per range
 #endif
-using SplitD64 = Tile<64, FA_SPLIT_D64>;
-using SplitD128 = Tile<128, FA_SPLIT_D128>;
+#ifndef FA_SPLIT_PLAN_D64_CAUSAL
+#define FA_SPLIT_PLAN_D64_CAUSAL 1024, 256
+#endif
+#ifndef FA_SPLIT_PLAN_D128_CAUSAL
+#define FA_SPLIT_PLAN_D128_CAUSAL 512, 1024
+#endif
+template <class T_, int TARGET_WGS_, int MIN_KEYS_>
+struct SplitRow {
+    using T = T_;
+    static constexpr int TARGET_WGS = TARGET_WGS_;
+    static constexpr int MIN_KEYS = MIN_KEYS_;
+};
+using SplitD64 = SplitRow<Tile<64, FA_SPLIT_D64>, FA_SPLIT_PLAN>;
+using SplitD64C = SplitRow<Tile<64, FA_SPLIT_D64_CAUSAL>, FA_SPLIT_PLAN_D64_CAUSAL>;
+using SplitD128 = SplitRow<Tile<128, FA_SPLIT_D128>, FA_SPLIT_PLAN>;
+using SplitD128C = SplitRow<Tile<128, FA_SPLIT_D128_CAUSAL>, FA_SPLIT_PLAN_D128_CAUSAL>;
+
+template <class F>
+auto with_split_row(int head_dim, bool causal, F&& f) {
+    if (head_dim == 64) return causal ? f(SplitD64C{}) : f(SplitD64{});
+    return causal ? f(SplitD128C{}) : f(SplitD128{});
+}
 
 struct SplitPlan {
     int n_splits;
@@ -2211,12 +2293,19 @@ struct SplitPlan {
 
 // Splits the key tiles of every query block into ranges of tiles_per_split tiles. With
 // requested == 0 the range length is the total number of (query block, key tile) pairs over
-// FA_SPLIT_TARGET_WGS (at least FA_SPLIT_MIN_TILES), so that about that many workgroups have
-// work; otherwise the longest query block's tiles are cut into `requested` ranges. Workspace:
-// fp32 O and LSE per split and row.
+// the row's TARGET_WGS (at least MIN_KEYS keys), so that about that many workgroups have work;
+// otherwise the longest query block's tiles are cut into `requested` ranges. Workspace: fp32 O
+// and LSE per split and row.
 SplitPlan split_plan(const fa_params& p, int requested) {
-    const int br = p.head_dim == 64 ? SplitD64::BR : SplitD128::BR;
-    const int bc = p.head_dim == 64 ? SplitD64::BC : SplitD128::BC;
+    struct Consts {
+        int br, bc, target_wgs, min_keys;
+    };
+    const Consts rc = with_split_row(p.head_dim, p.causal != 0, [](auto row) {
+        using R = decltype(row);
+        return Consts{R::T::BR, R::T::BC, R::TARGET_WGS, R::MIN_KEYS};
+    });
+    const int br = rc.br;
+    const int bc = rc.bc;
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
     const int nqb = g::ceil_div(p.seqlen, br);
     const int max_tiles = g::ceil_div(p.seqlen, bc);
@@ -2229,8 +2318,9 @@ SplitPlan split_plan(const fa_params& p, int requested) {
             pairs += g::num_kv_tiles(p.seqlen, qb * br, br, bc, p.causal != 0);
         }
         pairs *= bh;
-        const int64_t want = (pairs + FA_SPLIT_TARGET_WGS - 1) / FA_SPLIT_TARGET_WGS;
-        tps = static_cast<int>(std::min<int64_t>(std::max<int64_t>(FA_SPLIT_MIN_TILES, want),
+        const int64_t want = (pairs + rc.target_wgs - 1) / rc.target_wgs;
+        const int64_t min_tiles = g::ceil_div(rc.min_keys, bc);
+        tps = static_cast<int>(std::min<int64_t>(std::max<int64_t>(min_tiles, want),
                                                  max_tiles));
     }
     SplitPlan sp{};
@@ -2432,8 +2522,9 @@ int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits
     }
     const fa::Scale sc = fa::scale_of(p.softmax_scale);
     auto s = static_cast<hipStream_t>(stream);
-    return p.head_dim == 64 ? fa::splitkv<fa::SplitD64>(p, lse, sp, workspace, sc, s)
-                            : fa::splitkv<fa::SplitD128>(p, lse, sp, workspace, sc, s);
+    return fa::with_split_row(p.head_dim, p.causal != 0, [&](auto row) {
+        return fa::splitkv<typename decltype(row)::T>(p, lse, sp, workspace, sc, s);
+    });
 }
 
 }  // extern "C"

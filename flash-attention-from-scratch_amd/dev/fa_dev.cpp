@@ -1,13 +1,16 @@
 // fa_dev -- standalone driver of the attention forward, without Python or PyTorch.
 //
 //   fa_dev [B H N D causal iters variant] [--lib PATH] [--warmup-ms MS] [--seed S] [--json]
-//          [--std X] [--boost-keys FRAC:FACTOR]
+//          [--std X] [--boost-keys FRAC:FACTOR] [--splitkv S]
 //          defaults:  4 8 4096 128 0 20 opt,  --lib <this dir>/../fa/libfa_hip.so
 //   variant: base | baseline | opt | fp16acc
 //   --std X                 inputs ~ N(0, X^2) instead of N(0, 1)
 //   --boost-keys FRAC:FAC   multiply floor(FRAC * N) key rows of every head (a seeded random
 //                           choice) by FAC, as the benchmark's many-heads config does
 //                           (--std 0.5 --boost-keys 0.01:8): row maxima then jump mid-sequence
+//   --splitkv S             run the split-KV entry point (fa_flash_fwd_splitkv) with S key
+//                           ranges per query block (0 = the library's automatic plan) and a
+//                           workspace of the plan's size; the timing covers both launches
 //
 // Loads the kernel library at run time (dlopen) and calls only its C ABI (include/fa_hip.h),
 // as any foreign caller would: that lets the tuning sweep (dev/tune.py) time libraries built
@@ -54,6 +57,8 @@ struct Api {
     decltype(&fa_last_error) last_error = nullptr;
     decltype(&fa_tile_config) tile_config = nullptr;
     decltype(&fa_version) version = nullptr;
+    decltype(&fa_splitkv_plan) splitkv_plan = nullptr;
+    decltype(&fa_flash_fwd_splitkv) flash_fwd_splitkv = nullptr;
 };
 
 template <class F>
@@ -71,6 +76,8 @@ Api load_api(const std::string& path) {
     a.last_error = symbol<decltype(a.last_error)>(h, "fa_last_error");
     a.tile_config = symbol<decltype(a.tile_config)>(h, "fa_tile_config");
     a.version = symbol<decltype(a.version)>(h, "fa_version");
+    a.splitkv_plan = symbol<decltype(a.splitkv_plan)>(h, "fa_splitkv_plan");
+    a.flash_fwd_splitkv = symbol<decltype(a.flash_fwd_splitkv)>(h, "fa_flash_fwd_splitkv");
     return a;
 }
 
@@ -148,6 +155,7 @@ struct Options {
     float std = 1.0F;
     double boost_frac = 0.0;
     float boost = 1.0F;
+    int splitkv = -1;  // < 0: fa_flash_fwd; else fa_flash_fwd_splitkv with this many ranges
 };
 
 Options parse(int argc, char** argv) {
@@ -168,6 +176,9 @@ Options parse(int argc, char** argv) {
             o.seed = std::stoull(value());
         } else if (s == "--json") {
             o.json = true;
+        } else if (s == "--splitkv") {
+            o.splitkv = std::stoi(value());
+            if (o.splitkv < 0) throw std::invalid_argument("--splitkv must be >= 0");
         } else if (s == "--std") {
             o.std = std::stof(value());
         } else if (s == "--boost-keys") {
@@ -255,8 +266,22 @@ int run(const Options& o) {
     p.softmax_scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(o.head_dim)));
     p.causal = causal ? 1 : 0;
     p.variant = static_cast<uint8_t>(variant);
+    fa_splitkv_info plan{};
+    void* workspace = nullptr;
+    if (o.splitkv >= 0) {
+        if (api.splitkv_plan(&p, o.splitkv, &plan) != FA_OK) {
+            throw std::invalid_argument(api.last_error());
+        }
+        hip_check(hipMalloc(&workspace, plan.workspace_bytes), "hipMalloc workspace");
+        tile.block_q = plan.block_q;
+        tile.block_k = plan.block_k;
+    }
     auto launch = [&]() {
-        if (api.flash_fwd(&p, stream) != FA_OK) throw std::runtime_error(api.last_error());
+        const int rc = o.splitkv >= 0
+                           ? api.flash_fwd_splitkv(&p, nullptr, o.splitkv, workspace,
+                                                   plan.workspace_bytes, stream)
+                           : api.flash_fwd(&p, stream);
+        if (rc != FA_OK) throw std::runtime_error(api.last_error());
     };
 
     // One checked launch: rows 0, N/3 and N-1 of the first and last head, plus four more rows.
@@ -320,11 +345,12 @@ int run(const Options& o) {
             "\"N\": %d, \"D\": %d, \"causal\": %d, \"block_q\": %d, \"block_k\": %d, "
             "\"waves\": %d, \"max_abs_err\": %.3e, \"check\": \"%s\", \"iters\": %d, "
             "\"median_ms\": %.5f, \"mean_ms\": %.5f, \"min_ms\": %.5f, \"tflops\": %.2f, "
-            "\"frac_of_peak\": %.4f}\n",
+            "\"frac_of_peak\": %.4f, \"splitkv\": %d, \"n_splits\": %d, "
+            "\"tiles_per_split\": %d}\n",
             o.lib.c_str(), api.version(), o.variant.c_str(), o.batch, o.heads, o.seqlen,
             o.head_dim, causal ? 1 : 0, tile.block_q, tile.block_k, tile.waves, max_err,
             ok ? "ok" : "FAILED", o.iters, median, mean, static_cast<double>(sorted.front()), tf,
-            tf / kPeakTflops);
+            tf / kPeakTflops, o.splitkv, plan.num_splits, plan.tiles_per_split);
     } else {
         std::printf("%s B=%d H=%d N=%d D=%d causal=%d tile=%dx%d/%dw  max_abs_err=%.2e  "
                     "median=%.4f ms  %.1f TFLOPS (%.1f%% of peak)\n",
@@ -338,6 +364,7 @@ int run(const Options& o) {
     hip_check(hipEventDestroy(e1), "hipEventDestroy");
     hip_check(hipStreamDestroy(stream), "hipStreamDestroy");
     for (void* ptr : {dq, dk, dv, dout}) hip_check(hipFree(ptr), "hipFree");
+    if (workspace != nullptr) hip_check(hipFree(workspace), "hipFree workspace");
     return ok ? 0 : 1;
 }
 
@@ -349,7 +376,8 @@ int main(int argc, char** argv) {
     } catch (const std::invalid_argument& e) {
         std::fprintf(stderr,
                      "error: %s\nusage: fa_dev [B H N D causal iters variant] [--lib PATH] "
-                     "[--warmup-ms MS] [--seed S] [--json] [--std X] [--boost-keys FRAC:FAC]\n",
+                     "[--warmup-ms MS] [--seed S] [--json] [--std X] [--boost-keys FRAC:FAC] "
+                     "[--splitkv S]\n",
                      e.what());
         return 2;
     } catch (const std::exception& e) {

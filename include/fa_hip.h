@@ -84,7 +84,7 @@ int fa_flash_fwd_lse(const fa_params* params, float* lse, void* stream);
  * second kernel merges them by their LSEs. Same results as fa_flash_fwd within fp32 rounding
  * of the merge (not bitwise). No counterpart in the reference.
  * fa_splitkv_plan reports the ranges and the workspace size for num_splits (0 = automatic:
- * about a thousand workgroups with work); host-only. fa_flash_fwd_splitkv runs it: lse may be
+ * 256 to 1024 workgroups with work, by head_dim and causal); host-only. fa_flash_fwd_splitkv runs it: lse may be
  * NULL; workspace must be 16-byte aligned and hold at least workspace_bytes of the plan for the
  * same params and num_splits. Two launches on `stream`; allocates nothing. The variant field
  * is checked but every variant runs the same split tile. */

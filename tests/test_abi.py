@@ -187,21 +187,30 @@ def test_lse_entry_rejects_bad_lse_pointer():
 def test_splitkv_plan(b, h, n, d, causal):
     p = native.make_params(**{**GOOD, "batch": b, "heads": h, "seqlen": n, "head_dim": d,
                               "causal": causal})
-    bc = 64
+    # Partial-pass rows: the 16x16x32 ping-pong (256 query rows; 32 keys per tile at d=128, 64 at
+    # d=64) except causal d=64 (simple tile, 128 rows, 64 keys); the automatic plan keeps at
+    # least 512 keys per range when not causal, 1024 causal d=128, 256 causal d=64.
+    bq, bc, min_keys = {(128, False): (256, 32, 512), (128, True): (256, 32, 1024),
+                        (64, False): (256, 64, 512), (64, True): (128, 64, 256)}[(d, causal)]
     max_tiles = -(-n // bc)
     for req in (0, 1, 2, 3, 7, 100000):
         plan = native.splitkv_plan(p, req)
         ns, tps = plan["num_splits"], plan["tiles_per_split"]
-        assert plan["block_k"] == bc and plan["block_q"] == 128
+        assert plan["block_k"] == bc and plan["block_q"] == bq
         assert ns * tps >= max_tiles > (ns - 1) * tps       # ranges cover the keys, none empty
         assert plan["workspace_bytes"] == ns * b * h * n * (d + 1) * 4
         if req:
             assert ns <= req
         else:
-            assert tps >= min(4, max_tiles)
-    if (b, h, n, d, causal) == (1, 2, 16384, 128, False):
-        # 2 heads x 128 query blocks x 256 key tiles / 1024 target workgroups = 64 tiles
-        assert native.splitkv_plan(p, 0)["tiles_per_split"] == 64
+            assert tps >= min(min_keys // bc, max_tiles)
+    known = {
+        # 2 heads x 64 query blocks x 512 key tiles / 256 target workgroups = 256 tiles
+        (1, 2, 16384, 128, False): 256,
+        # causal: 2 heads x 8 x (1 + ... + 64) = 33280 (block, tile) pairs / 512 -> 65 tiles
+        (1, 2, 16384, 128, True): 65,
+    }
+    if (b, h, n, d, causal) in known:
+        assert native.splitkv_plan(p, 0)["tiles_per_split"] == known[(b, h, n, d, causal)]
 
 
 def test_splitkv_entry_rejects_bad_workspace():

@@ -92,6 +92,8 @@ SPLIT_CASES = [
     (1, 2, 3001, 128, True, 0), (1, 2, 3001, 128, True, 5), (1, 2, 3001, 128, False, 1),
     (1, 3, 2048, 128, False, 7), (1, 1, 17, 64, True, 0), (1, 1, 1, 128, False, 4),
     (1, 2, 700, 64, True, 1000),
+    # automatic plans with several ranges per query block (steady ping-pong state per range)
+    (1, 4, 4097, 64, True, 0), (1, 1, 5000, 128, False, 0), (1, 1, 6000, 128, True, 0),
 ]
 
 
