@@ -185,6 +185,22 @@ constexpr int wave_unmasked_tiles(int n, int qw, int block_k, int n_act, bool ca
     return t < n_act ? t : n_act;
 }
 
+// Split-KV: the key tiles [begin, begin + count) of range `split` of a query block that visits
+// n_all tiles. The block is cut into ceil(n_all / tps) ranges (the count the combine kernel
+// reads for its rows) of near-equal length (floor or ceil of n_all / ranges, at most tps), so
+// that no range is a short remainder; count = 0 for a range the block does not have.
+struct KeyRange {
+    int begin;
+    int count;
+};
+constexpr KeyRange split_range(int n_all, int tps, int split) {
+    const int ranges = ceil_div(n_all, tps);
+    if (split >= ranges) return KeyRange{0, 0};
+    const long long b = static_cast<long long>(split) * n_all / ranges;
+    const long long e = static_cast<long long>(split + 1) * n_all / ranges;
+    return KeyRange{static_cast<int>(b), static_cast<int>(e - b)};
+}
+
 // Workgroup id -> (batch*head index, query block). Consecutive ids share the query block and
 // walk the heads; the hardware deals consecutive ids round-robin to the 8 XCDs, so each XCD
 // keeps a fixed subset of heads (whose K/V then stay in that XCD's L2) when B*H is a multiple

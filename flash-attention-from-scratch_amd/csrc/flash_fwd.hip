@@ -428,7 +428,7 @@ __device__ __forceinline__ void store_partial(float* op, float* lp, int qrow, in
 // ---- kernel, simple schedule (the "baseline" build) -----------------------------------------
 // Per tile: barrier, prefetch tile j+1, then S = QK^T, softmax, O += PV in sequence.
 // SPLIT (split-KV): block id = split * (B*H*query blocks) + work item; the workgroup runs key
-// tiles [split * tiles_per_split, +tiles_per_split) of its query block and writes the partial
+// range `split` of its query block (geom::split_range) and writes the partial
 // O and LSE of each row to o_part / lse_part (layout [split][b*h][n][d] and [split][b*h][n]);
 // a workgroup whose range is empty exits at once (the combine kernel never reads it).
 template <class T, bool CAUSAL, bool SPLIT = false>
@@ -453,11 +453,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const int qw = q0 + wave * 32;       // first query of this wave
     const int qrow = qw + (lane & 31);   // this lane's query
     const int n_all = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-    const int j_begin = SPLIT ? split * tiles_per_split : 0;
-    const int n_tiles = SPLIT ? min(n_all, j_begin + tiles_per_split) : n_all;
+    const g::KeyRange range = SPLIT ? g::split_range(n_all, tiles_per_split, split)
+                                    : g::KeyRange{0, n_all};
+    const int j_begin = range.begin;
+    const int n_tiles = range.begin + range.count;  // absolute: tiles [j_begin, n_tiles)
     // Workgroup-uniform exit of an empty split. Compiled only into the split-KV build: in the
     // plain one the extra exit costs the causal d=64 tile 30 VGPRs (and half its occupancy).
-    if (SPLIT && j_begin >= n_tiles) return;
+    if (SPLIT && range.count == 0) return;
 
     // LDS: [K0 | K1 | V0 | V1]; buffer b of K at b*TILE_BYTES, of V at (2+b)*TILE_BYTES.
     auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
@@ -1740,18 +1742,20 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const int q0 = w.qb * T::BR;
     const int qw = q0 + wave * 32;  // first query of this wave (Q loads, O stores)
-    // Split-KV: the workgroup runs key tiles [j_begin, j_begin + tiles_per_split) of its query
-    // block as if the keys started at key0: K/V pointers, the sequence end nk and the query
-    // position qk used by the masks are all taken relative to key0.
+    // Split-KV: the workgroup runs its query block's key range `split` (geom::split_range) as
+    // if the keys started at key0: K/V pointers, the sequence end nk and the query position qk
+    // used by the masks are all taken relative to key0.
     const int n_all = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-    const int j_begin = SPLIT ? split * tiles_per_split : 0;
-    if (SPLIT && j_begin >= n_all) return;  // workgroup-uniform: empty range
+    const g::KeyRange range = SPLIT ? g::split_range(n_all, tiles_per_split, split)
+                                    : g::KeyRange{0, n_all};
+    if (SPLIT && range.count == 0) return;  // workgroup-uniform: no such range
+    const int j_begin = range.begin;
     const int key0 = j_begin * T::BC;
     const int nk = n - key0;
     const int qk = qw - key0;
     const f16* kh = k + head + static_cast<size_t>(key0) * T::D;
     const f16* vh = v + head + static_cast<size_t>(key0) * T::D;
-    const int n_tiles = SPLIT ? min(n_all - j_begin, tiles_per_split) : n_all;
+    const int n_tiles = range.count;
     // (a split can start right of all of this wave's queries: no active tile then)
     const int n_act = (SPLIT && CAUSAL && qk + 31 < 0)
                           ? 0

@@ -43,6 +43,11 @@ int geom_wave_active_tiles(int n, int qw, int rows, int block_k, int n_tiles, in
 int geom_wave_unmasked_tiles(int n, int qw, int block_k, int n_act, int causal) {
     return g::wave_unmasked_tiles(n, qw, block_k, n_act, causal != 0);
 }
+void geom_split_range(int n_all, int tps, int split, int* begin, int* count) {
+    const g::KeyRange r = g::split_range(n_all, tps, split);
+    *begin = r.begin;
+    *count = r.count;
+}
 void geom_work_of(int block_id, int bh_count, int n_qblocks, int causal, int* bh, int* qb) {
     const g::Work w = g::work_of(block_id, bh_count, n_qblocks, causal != 0);
     *bh = w.bh;

@@ -26,6 +26,7 @@ LIB = Path(__file__).resolve().parent / "geometry" / "libfa_geom.so"
 def geo():
     so = ctypes.CDLL(str(LIB))
     so.geom_work_of.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
+    so.geom_split_range.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 2
     return so
 
 
@@ -364,3 +365,24 @@ def test_work_map_is_a_bijection(geo, causal):
                 assert qb.value <= prev  # longest (highest) query blocks launch first
             prev = qb.value
         assert len(seen) == bhc * nqb
+
+
+def test_split_ranges_partition_each_query_block(geo):
+    """Split-KV: the ranges of a query block with n_all key tiles are exactly the
+    ceil(n_all / tps) ranges the combine kernel reads, non-empty, at most tps tiles each,
+    within one tile of each other in length, and together cover [0, n_all) once, in order."""
+    b, c = ctypes.c_int(), ctypes.c_int()
+    for n_all in (1, 2, 3, 7, 8, 9, 33, 64, 65, 100, 512, 4097):
+        for tps in (1, 2, 3, 4, 16, 32, 33, 65, 128, 600):
+            ranges = -(-n_all // tps)
+            got = []
+            for split in range(ranges + 3):
+                geo.geom_split_range(n_all, tps, split, ctypes.byref(b), ctypes.byref(c))
+                if split >= ranges:
+                    assert c.value == 0
+                    continue
+                got.append((b.value, c.value))
+            assert [x[0] for x in got] == [sum(x[1] for x in got[:i]) for i in range(len(got))]
+            assert sum(x[1] for x in got) == n_all
+            lens = [x[1] for x in got]
+            assert min(lens) >= 1 and max(lens) <= tps and max(lens) - min(lens) <= 1
