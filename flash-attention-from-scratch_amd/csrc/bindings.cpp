@@ -3,6 +3,11 @@
 // HIP stream of torch. `forward` mirrors the reference binding; `forward_lse` and
 // `forward_splitkv` are additions of this library (no reference counterpart).
 //
+// Grids too small to fill the GPU (few heads, long sequences): where the library's split-KV
+// plan says its split path is the faster one (fa_splitkv_info.preferred), `forward` and
+// `forward_lse` run it, with the workspace taken from torch's caching allocator;
+// fa_flash_fwd itself stays a single allocation-free launch.
+//
 // Same signature, defaults and error conditions as the reference binding
 // (csrc/bindings.cpp:28-73): RuntimeError with the words "CUDA", "float16", "contiguous",
 // "[B, H, N, D]", "same shape", "same device" for bad tensors and "variant" for an unknown
@@ -72,6 +77,17 @@ hipStream_t stream_of(const torch::Tensor& q) {
     return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
 }
 
+// Runs the split-KV path if the library prefers it for these params; false (nothing launched)
+// otherwise, including for params the plan rejects (fa_flash_fwd then reports them).
+bool splitkv_if_preferred(const fa_params& p, float* lse, const torch::Tensor& q) {
+    fa_splitkv_info info{};
+    if (fa_splitkv_plan(&p, 0, &info) != FA_OK || info.preferred == 0) return false;
+    auto ws = torch::empty({static_cast<int64_t>(info.workspace_bytes / 4)},
+                           q.options().dtype(torch::kFloat));
+    check_rc(fa_flash_fwd_splitkv(&p, lse, 0, ws.data_ptr(), info.workspace_bytes, stream_of(q)));
+    return true;
+}
+
 torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
                       bool causal, std::optional<double> softmax_scale,
                       const std::string& variant) {
@@ -82,9 +98,11 @@ torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torc
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     auto o = torch::empty_like(q);
     const fa_params p = make_params(q, k, v, o, causal, softmax_scale, var);
-    // N = 0 (or any empty dimension) returns an empty output without a launch
-    // (csrc/bindings.cpp:60-62).
-    if (q.numel() == 0) return o;
+    // N = 0 returns an empty output without a launch (csrc/bindings.cpp:60-62); any other empty
+    // dimension (B, H or D = 0) reaches the launcher, which rejects it with ValueError
+    // ("batch, heads and seqlen must be positive", "head_dim must be 64 or 128, got 0").
+    if (q.size(2) == 0) return o;
+    if (splitkv_if_preferred(p, nullptr, q)) return o;
     check_rc(fa_flash_fwd(&p, stream_of(q)));
     return o;
 }
@@ -101,7 +119,9 @@ std::tuple<torch::Tensor, torch::Tensor> forward_lse(const torch::Tensor& q,
     auto o = torch::empty_like(q);
     auto lse = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(torch::kFloat));
     const fa_params p = make_params(q, k, v, o, causal, softmax_scale, var);
-    if (q.numel() == 0) return {o, lse};
+    if (q.size(2) == 0) return {o, lse};
+    // Same path choice as forward, so that O is bitwise forward's.
+    if (splitkv_if_preferred(p, lse.data_ptr<float>(), q)) return {o, lse};
     check_rc(fa_flash_fwd_lse(&p, lse.data_ptr<float>(), stream_of(q)));
     return {o, lse};
 }
@@ -119,7 +139,7 @@ std::tuple<torch::Tensor, torch::Tensor> forward_splitkv(const torch::Tensor& q,
     auto o = torch::empty_like(q);
     auto lse = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(torch::kFloat));
     fa_params p = make_params(q, k, v, o, causal, softmax_scale, FA_VARIANT_OPT);
-    if (q.numel() == 0) return {o, lse};
+    if (q.size(2) == 0) return {o, lse};
     fa_splitkv_info info{};
     check_rc(fa_splitkv_plan(&p, static_cast<int32_t>(num_splits), &info));
     auto ws = torch::empty({static_cast<int64_t>(info.workspace_bytes / 4)},

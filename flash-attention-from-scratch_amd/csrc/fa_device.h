@@ -111,6 +111,28 @@ __device__ __forceinline__ f16x8 pack8(float a0, float a1, float a2, float a3, f
     return f16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
+// 16-byte output stores from two lanes that hold halves of the same row. v_permlane16_swap
+// swaps the odd 16-lane rows of its first operand with the even rows of its second (lanes l and
+// l ^ 16); v_permlane32_swap swaps lanes 32..63 of the first operand with lanes 0..31 of the
+// second (l and l ^ 32). Lane l of the lower row of a pair thus receives {a[l], a[partner]} and
+// lane l of the upper row {b[partner], b[l]}: if the lower lane holds 4 consecutive values a
+// and the partner the 4 that follow them, and likewise for b one block further, each lane ends
+// with 8 consecutive values of one block (a for the lower lane, b for the upper one).
+__device__ __forceinline__ f16x8 pair_swap16(f16x4 a, f16x4 b) {
+    const auto ua = __builtin_bit_cast(uint2, a);
+    const auto ub = __builtin_bit_cast(uint2, b);
+    const auto r0 = __builtin_amdgcn_permlane16_swap(ua.x, ub.x, false, false);
+    const auto r1 = __builtin_amdgcn_permlane16_swap(ua.y, ub.y, false, false);
+    return __builtin_bit_cast(f16x8, uint4{r0[0], r1[0], r0[1], r1[1]});
+}
+__device__ __forceinline__ f16x8 pair_swap32(f16x4 a, f16x4 b) {
+    const auto ua = __builtin_bit_cast(uint2, a);
+    const auto ub = __builtin_bit_cast(uint2, b);
+    const auto r0 = __builtin_amdgcn_permlane32_swap(ua.x, ub.x, false, false);
+    const auto r1 = __builtin_amdgcn_permlane32_swap(ua.y, ub.y, false, false);
+    return __builtin_bit_cast(f16x8, uint4{r0[0], r1[0], r0[1], r1[1]});
+}
+
 __device__ __forceinline__ f16x4 pack4(float a0, float a1, float a2, float a3) {
     const f16x2 p0 = __builtin_convertvector(f32x2{a0, a1}, f16x2);
     const f16x2 p1 = __builtin_convertvector(f32x2{a2, a3}, f16x2);

@@ -45,68 +45,6 @@
 #include "fa_geometry.h"
 #include "fa_hip.h"
 
-// Clock probe (only in the fa/libfa_hip_clock.so build, -DFA_CLOCK_PROBE=1): each workgroup of
-// the main kernels records its shader cycles and its 100 MHz real time, from which the clock the
-// kernel actually ran at follows, plus its start on the chip-wide 100 MHz counter and where it
-// ran (HW_ID: CU, shader array and engine; XCC_ID: the chiplet), for a per-CU timeline.
-// Compiled out of the library proper.
-#ifndef FA_CLOCK_PROBE
-#define FA_CLOCK_PROBE 0
-#endif
-#if FA_CLOCK_PROBE
-__device__ unsigned long long g_fa_clock[65536][4];
-#define FA_CLOCK_BEGIN()                                                  \
-    const unsigned long long fa_c0 = __builtin_amdgcn_s_memtime();        \
-    const unsigned long long fa_r0 = __builtin_amdgcn_s_memrealtime()
-#define FA_CLOCK_END()                                                    \
-    do {                                                                  \
-        const unsigned long long fa_c1 = __builtin_amdgcn_s_memtime();    \
-        const unsigned long long fa_r1 = __builtin_amdgcn_s_memrealtime(); \
-        if (threadIdx.x == 0 && blockIdx.x < 65536) {                     \
-            unsigned fa_hw, fa_xcc;                                       \
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)\n"        \
-                         "s_getreg_b32 %1, hwreg(HW_REG_XCC_ID)"           \
-                         : "=s"(fa_hw), "=s"(fa_xcc));                     \
-            g_fa_clock[blockIdx.x][0] = fa_c1 - fa_c0;                    \
-            g_fa_clock[blockIdx.x][1] = fa_r1 - fa_r0;                    \
-            g_fa_clock[blockIdx.x][2] = fa_r0;                            \
-            g_fa_clock[blockIdx.x][3] =                                   \
-                (static_cast<unsigned long long>(fa_xcc) << 32) | fa_hw;  \
-        }                                                                 \
-    } while (0)
-// Ping-pong phase timing (same build): per wave, shader cycles summed over the steady tiles
-// for [0] issuing the softmax phase, [1] its end-of-phase wait and barrier, [2] issuing the
-// matrix phase, [3] its wait and barrier; [4] steady tiles, [5] cycles of the whole wave.
-// The stamps sit next to the phase-end waits, whose lgkmcnt(0) the s_memtime results need.
-__device__ unsigned long long g_fa_phase[8192][8][6];
-#define FA_PHASE_DECL()                                   \
-    unsigned long long fa_ph[6] = {0, 0, 0, 0, 0, 0};     \
-    const unsigned long long fa_pt0 = __builtin_amdgcn_s_memtime()
-#define FA_PHASE_T(var) const unsigned long long var = __builtin_amdgcn_s_memtime()
-#define FA_PHASE_TILE(ta, tb, tc, td, te) \
-    do {                                  \
-        fa_ph[0] += (tb) - (ta);          \
-        fa_ph[1] += (tc) - (tb);          \
-        fa_ph[2] += (td) - (tc);          \
-        fa_ph[3] += (te) - (td);          \
-        fa_ph[4] += 1;                    \
-    } while (0)
-#define FA_PHASE_STORE(wave, lane)                                               \
-    do {                                                                         \
-        fa_ph[5] = __builtin_amdgcn_s_memtime() - fa_pt0;                        \
-        if ((lane) == 0 && blockIdx.x < 8192) {                                  \
-            for (int fa_i = 0; fa_i < 6; ++fa_i) g_fa_phase[blockIdx.x][wave][fa_i] = fa_ph[fa_i]; \
-        }                                                                        \
-    } while (0)
-#else
-#define FA_CLOCK_BEGIN() static_cast<void>(0)
-#define FA_CLOCK_END() static_cast<void>(0)
-#define FA_PHASE_DECL() static_cast<void>(0)
-#define FA_PHASE_T(var) static_cast<void>(0)
-#define FA_PHASE_TILE(ta, tb, tc, td, te) static_cast<void>(0)
-#define FA_PHASE_STORE(wave, lane) static_cast<void>(0)
-#endif
-
 namespace fa {
 namespace {
 
@@ -122,13 +60,11 @@ namespace g = fa::geom;
 #endif
 
 // Main-loop schedules: SIMPLE (flash_fwd_kernel), PIPE (flash_fwd_pipelined: QK of tile j+1
-// interleaved with the softmax of tile j in each wave), PINGPONG (flash_fwd_pingpong: two
-// groups of waves alternate between an MFMA-only phase and a softmax phase), KSPLIT
-// (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles), PINGPONG16
-// (flash_fwd_pingpong16: the ping-pong schedule on 16x16x32 MFMAs; the table's long-sequence
-// rows; PINGPONG stays for A/B builds), SIMPLE16 (flash_fwd_simple16: the simple schedule on
-// 16x16x32 MFMAs).
-enum Sched { SIMPLE = 0, PIPE = 1, PINGPONG = 2, KSPLIT = 3, PINGPONG16 = 4, SIMPLE16 = 5 };
+// interleaved with the softmax of tile j in each wave), KSPLIT (flash_fwd_ksplit: two waves per
+// 32 query rows on alternate key tiles), PINGPONG16 (flash_fwd_pingpong16: two groups of waves
+// alternate between an MFMA-only phase and a softmax phase, on 16x16x32 MFMAs; the table's
+// long-sequence rows). The values are those the -D tile overrides name.
+enum Sched { SIMPLE = 0, PIPE = 1, KSPLIT = 3, PINGPONG16 = 4 };
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
@@ -143,8 +79,8 @@ struct Tile {
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
-    static constexpr bool M16 = SCHED == PINGPONG16 || SCHED == SIMPLE16;  // 16x16x32 layouts
-    static constexpr int NBUF = (SCHED == PINGPONG || SCHED == PINGPONG16) ? 3 : 2;  // per K, V
+    static constexpr bool M16 = SCHED == PINGPONG16;      // 16x16x32 layouts
+    static constexpr int NBUF = SCHED == PINGPONG16 ? 3 : 2;  // per K, V
     static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES * KS;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
@@ -375,24 +311,34 @@ __device__ __forceinline__ float row_lse2(float m_run, float l_tot) {
 }
 
 // O = acc / l as fp16 (RNE) for the lane's query row, if it is < n. The lane holds feature
-// columns 32*db + 8*rq + 4*(lane/32) + 0..3: one 8-byte store each. If lse_h is not null, the
-// row's natural-log LSE (log of the sum of exp(scale * q.k) over its keys) goes to lse_h[qrow].
+// columns 32*db + 8*rq + 4*(lane/32) + 0..3; the two wave halves, which hold the same query,
+// trade half of them (pair_swap32) so that each lane writes 8 consecutive features per 16-byte
+// store. If lse_h is not null, the row's natural-log LSE (log of the sum of exp(scale * q.k)
+// over its keys) goes to lse_h[qrow].
 template <class T>
 __device__ __forceinline__ void store_o_tot(f16* oh, float* lse_h, int qrow, int n, int lane,
                                             float m_run, float l_tot,
                                             const f32x16 (&oacc)[T::DB]) {
     const float inv = (l_tot > 0.0F) ? (1.0F / l_tot) : 0.0F;
-    if (qrow >= n) return;
-    if (lse_h != nullptr && lane < 32) lse_h[qrow] = row_lse2(m_run, l_tot) * kLn2;
-    f16* dst = oh + static_cast<size_t>(qrow) * T::D + 4 * (lane >> 5);
+    f16x8 out[T::DB][2];
 #pragma unroll
     for (int db = 0; db < T::DB; ++db)
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
+        for (int r = 0; r < 2; ++r) {
             const f32x16& a = oacc[db];
-            *reinterpret_cast<f16x4*>(dst + 32 * db + 8 * rq) = pack4(
-                a[4 * rq] * inv, a[4 * rq + 1] * inv, a[4 * rq + 2] * inv, a[4 * rq + 3] * inv);
+            out[db][r] = pair_swap32(
+                pack4(a[8 * r] * inv, a[8 * r + 1] * inv, a[8 * r + 2] * inv, a[8 * r + 3] * inv),
+                pack4(a[8 * r + 4] * inv, a[8 * r + 5] * inv, a[8 * r + 6] * inv,
+                      a[8 * r + 7] * inv));
         }
+    if (qrow >= n) return;
+    if (lse_h != nullptr && lane < 32) lse_h[qrow] = row_lse2(m_run, l_tot) * kLn2;
+    // lower half: features 32db + 16r + 0..7, upper half: 32db + 16r + 8..15
+    f16* dst = oh + static_cast<size_t>(qrow) * T::D + 8 * (lane >> 5);
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) *reinterpret_cast<f16x8*>(dst + 32 * db + 16 * r) = out[db][r];
 }
 
 // Same, from the lane's partial row sum (its keys of each 32-key block; the two wave halves
@@ -438,7 +384,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
     float* __restrict__ lse_part) {
     __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
-    FA_CLOCK_BEGIN();
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -505,21 +450,26 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
                    m_run, l_run, oacc);
     }
-    FA_CLOCK_END();
 }
 
 // Split-KV combine: for each row, LSE = log2-sum-exp2 of the splits' base-2 LSEs, and
 // O = sum_s 2^(lse_s - LSE) O_s. Splits past a causal row block's last key tile were never
-// run and are not read. One thread per 4 features of a row.
+// run and are not read. One thread per 8 features of a row (one 16-byte store).
+template <int D>
+struct CombineGeom {
+    static constexpr int TPR = D / 8;          // threads per row
+    static constexpr int ROWS = 256 / TPR;     // rows per 256-thread block
+};
 template <int D>
 __global__ __launch_bounds__(256) void flash_fwd_combine(
     const float* __restrict__ o_part, const float* __restrict__ lse_part, f16* __restrict__ o,
     float* __restrict__ lse, int n, int bh_count, int n_splits, int tiles_per_split, int causal,
     int block_q, int block_k) {
-    constexpr int TPR = D / 4;  // threads per row
-    const long long row = static_cast<long long>(blockIdx.x) * (256 / TPR) + threadIdx.x / TPR;
+    constexpr int TPR = CombineGeom<D>::TPR;
+    const long long row = static_cast<long long>(blockIdx.x) * CombineGeom<D>::ROWS +
+                          threadIdx.x / TPR;
     if (row >= static_cast<long long>(bh_count) * n) return;
-    const int c = 4 * (threadIdx.x % TPR);
+    const int c = 8 * (threadIdx.x % TPR);
     const int i = static_cast<int>(row % n);
     int splits = n_splits;
     if (causal) {
@@ -530,16 +480,18 @@ __global__ __launch_bounds__(256) void flash_fwd_combine(
     float m = -INFINITY;
     for (int s = 0; s < splits; ++s) m = fmaxf(m, lse_part[s * plane + row]);
     float wsum = 0.0F;
-    f32x4 acc{};
+    f32x4 acc0{}, acc1{};
     for (int s = 0; s < splits; ++s) {
         const float wgt = exp2_fast(lse_part[s * plane + row] - m);
-        const f32x4 x = *reinterpret_cast<const f32x4*>(o_part + (s * plane + row) * D + c);
+        const float* src = o_part + (s * plane + row) * D + c;
         wsum += wgt;
-        acc += wgt * x;
+        acc0 += wgt * *reinterpret_cast<const f32x4*>(src);
+        acc1 += wgt * *reinterpret_cast<const f32x4*>(src + 4);
     }
     const float inv = 1.0F / wsum;  // >= 1: the split holding the row's max weighs 1
-    *reinterpret_cast<f16x4*>(o + row * D + c) = pack4(acc[0] * inv, acc[1] * inv, acc[2] * inv,
-                                                       acc[3] * inv);
+    *reinterpret_cast<f16x8*>(o + row * D + c) =
+        pack8(acc0[0] * inv, acc0[1] * inv, acc0[2] * inv, acc0[3] * inv, acc1[0] * inv,
+              acc1[1] * inv, acc1[2] * inv, acc1[3] * inv);
     if (lse != nullptr && c == 0) lse[row] = (m + __builtin_amdgcn_logf(wsum)) * kLn2;
 }
 
@@ -558,7 +510,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     static_assert(T::KS == 2, "two key halves");
     // Tiles: half h, buffer b: K at (2h + b) * 2 tiles, V right after. Reused by the merge.
     __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
-    FA_CLOCK_BEGIN();
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -659,7 +610,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
         store_o_tot<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n,
                        lane, m_new, l_new, oacc);
     }
-    FA_CLOCK_END();
 }
 
 // Scheduler pattern: N times {one MFMA, then up to VALU_PER VALU instructions}. Masks of
@@ -865,7 +815,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
-    FA_CLOCK_BEGIN();
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -969,18 +918,17 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
                                 oacc, scale_log2, m_run, l_run);
     store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
                m_run, l_run, oacc);
-    FA_CLOCK_END();
 }
 
-// ---- kernel, ping-pong schedule ---------------------------------------------------------------
+// ---- ping-pong schedule: phase protocol ---------------------------------------------------------
 // Eight waves, two groups of four: the hardware deals the waves of a workgroup round-robin to
 // the four SIMDs of the CU, so waves w and w+4 share a SIMD. Every wave alternates two phases
 // per K/V tile, separated by workgroup barriers:
 //   softmax phase S_j: fragment reads of K_{j+1} and V_j from LDS (for the next phase),
 //                      interleaved with the softmax of tile j (P_j, row sums, rare exact
 //                      rescale of O) on the VALU;
-//   matrix phase  M_j: S_{j+1} = K_{j+1} Q^T and O += P_j V_j (sixteen MFMAs at D = 128) and
-//                      the wave's share of the K/V refill.
+//   matrix phase  M_j: S_{j+1} = K_{j+1} Q^T and O += P_j V_j (32 MFMAs per wave) and the
+//                      wave's share of the K/V refill.
 // Group 1 runs one phase behind group 0 (group 0: S_j in global phase 2j, M_j in 2j+1), so in
 // every phase one wave of each SIMD feeds the matrix pipe while the other works on the VALU and
 // the LDS, and only four waves read LDS at a time, each a whole phase ahead of its use.
@@ -989,27 +937,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
 // the barrier that ends the next-but-one odd phase, so each wave waits with vmcnt(2) (its two
 // newest requests stay in flight) at the end of its odd phases. Each tile is thus requested 3
 // or 4 phases before its first read, and replaces a tile whose last read was in an earlier
-// phase. Tiles that need masking, the last tile and causal diagonal tiles go through
-// general_tiles afterwards.
+// phase. Diagonal and tail tiles are masked inside the steady phases; only the last tile, which
+// has no successor to prefetch, goes through general_tiles16 afterwards.
 #ifndef FA_PP_PRIO
 #define FA_PP_PRIO 1
 #endif
-#ifndef FA_PP_MASKED_STEADY
-#define FA_PP_MASKED_STEADY 1
-#endif
-
-#ifndef FA_PP_EXPS_FIRST
-#define FA_PP_EXPS_FIRST 1
-#endif
-
 // Scheduler pattern: N times {R DS reads, V VALU instructions} (sched_group_barrier masks
 // 0x100 DS read, 0x002 VALU | 0x400 transcendental).
-#ifndef FA_PP_READS_PER
-#define FA_PP_READS_PER 3
-#endif
-#ifndef FA_PP_VALU_PER
-#define FA_PP_VALU_PER 6
-#endif
 template <int R, int V, int N>
 __device__ __forceinline__ void sched_reads_valu() {
 #pragma unroll
@@ -1035,268 +969,9 @@ __device__ __forceinline__ void end_phase() {
     asm volatile("" ::: "memory");
 }
 
-// Softmax of a mask-free tile against the running max m (see qk_softmax_optimistic): P in
-// fp16, and l += row sum unless some p overflowed fp16, in which case `overflow` is set
-// (wave-uniform) and the caller redoes the tile exactly. The row sum runs in two independent
-// v_dot2 chains.
-template <class T>
-__device__ __forceinline__ void softmax_optimistic(const f32x16 (&s)[T::NB], float scale_log2,
-                                                   float m_run, float& l_run, bool& overflow,
-                                                   f16x8 (&p)[T::NB][2]) {
-    float sum0 = 0.0F;
-    float sum1 = 0.0F;
-#if FA_PP_EXPS_FIRST
-    // All exponentials of the tile first, then the packs and sums (a pack right behind the
-    // exponentials it reads waits on their latency).
-    float e[T::NB][16];
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) e[nb][r] = exp2_fast(fmaf(s[nb][r], scale_log2, -m_run));
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) {
-        p[nb][0] = pack8(e[nb][0], e[nb][1], e[nb][2], e[nb][3], e[nb][4], e[nb][5], e[nb][6],
-                         e[nb][7]);
-        p[nb][1] = pack8(e[nb][8], e[nb][9], e[nb][10], e[nb][11], e[nb][12], e[nb][13],
-                         e[nb][14], e[nb][15]);
-    }
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) {
-        sum0 = sum8_f16(p[nb][0], sum0);
-        sum1 = sum8_f16(p[nb][1], sum1);
-    }
-#else
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) {
-        float e[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) e[r] = exp2_fast(fmaf(s[nb][r], scale_log2, -m_run));
-        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
-        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
-        sum0 = sum8_f16(p[nb][0], sum0);
-        sum1 = sum8_f16(p[nb][1], sum1);
-    }
-#endif
-    const float sum = sum0 + sum1;
-    overflow = wave_any(!(sum < INFINITY));
-    const float l_new = l_run + sum;
-    l_run = overflow ? l_run : l_new;
-}
-
-// Matrix phase: S^T_{j+1} = K_{j+1} Q^T (one chain of KK MFMAs per 32-key block) interleaved
-// with O^T += V_j^T P_j^T (2*DB MFMAs per block, DB independent chains). `mid` (the refill)
-// is issued after the first two pairs, when the matrix pipe already has work queued.
-template <class T, class Mid>
-__device__ __forceinline__ void matrix_phase(const f16x8 (&kf)[T::NB][T::KK],
-                                             const f16x8 (&qf)[T::KK],
-                                             const f16x8 (&vf)[T::NB][2][T::DB],
-                                             const f16x8 (&p)[T::NB][2], f32x16 (&s)[T::NB],
-                                             f32x16 (&oacc)[T::DB], Mid&& mid) {
-    constexpr int NQK = T::NB * T::KK;
-    constexpr int NPV = T::NB * 2 * T::DB;
-    constexpr int NI = NQK > NPV ? NQK : NPV;
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) s[nb] = f32x16{};
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        if (i < NQK) {
-            const int nb = i / T::KK;
-            const int kk = i % T::KK;
-            s[nb] = mfma32(kf[nb][kk], qf[kk], s[nb]);
-        }
-        if (i < NPV) {
-            const int nb = i / (2 * T::DB);
-            const int h = (i / T::DB) % 2;
-            const int db = i % T::DB;
-            oacc[db] = mfma32(vf[nb][h][db], p[nb][h], oacc[db]);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // keep the alternation
-        if (i == 1) {
-            mid();
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-}
-
-template <class T, bool CAUSAL>
-__global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
-    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
-    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
-    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
-    float* /*lse_part*/) {
-    static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
-    static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
-    static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
-    FA_CLOCK_BEGIN();
-    // Separate LDS objects per buffer, as in flash_fwd_pipelined.
-    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v_lds2[T::TILE_BYTES];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = wave_uniform(threadIdx.x >> 6);
-    const int grp = wave >> 2;
-    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
-    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
-    const f16* kh = k + head;
-    const f16* vh = v + head;
-    const int q0 = w.qb * T::BR;
-    const int qw = q0 + wave * 32;
-    const int qrow = qw + (lane & 31);
-    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-    const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
-    // Steady tiles are the same for the whole workgroup (both groups must pass the same
-    // barriers). With FA_PP_MASKED_STEADY every tile but the last runs in the steady phases,
-    // diagonal and tail tiles masked there (a wave whose rows are all left of a tile computes
-    // it to p = 0); otherwise only those that wave 0, the one with the fewest, can take
-    // without a mask and with an active successor.
-    const int n_act0 = g::wave_active_tiles(n, q0, 32, T::BC, n_tiles, CAUSAL);
-    const int n_steady =
-        FA_PP_MASKED_STEADY ? max(0, n_tiles - 1)
-                            : max(0, min(g::wave_unmasked_tiles(n, q0, T::BC, n_act0, CAUSAL),
-                                         n_act0 - 1));
-
-    // Buffer b (compile-time in the steady loop, so the compiler can tell the objects apart).
-    auto kbuf = [&](auto b) {
-        constexpr int B = decltype(b)::value;
-        return B == 0 ? k_lds0 : (B == 1 ? k_lds1 : k_lds2);
-    };
-    auto vbuf = [&](auto b) {
-        constexpr int B = decltype(b)::value;
-        return B == 0 ? v_lds0 : (B == 1 ? v_lds1 : v_lds2);
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
-
-    const TileDma<T> dma(wave, lane);
-    // Prologue: K_0, K_1, K_2, V_0, V_1 (tiles past the end read as zeros and are never used).
-    load_tile<T>(kh, 0, n, kbuf(I0{}), dma);
-    load_tile<T>(vh, 0, n, vbuf(I0{}), dma);
-    load_tile<T>(kh, T::BC, n, kbuf(I1{}), dma);
-    load_tile<T>(kh, 2 * T::BC, n, kbuf(I2{}), dma);
-    load_tile<T>(vh, T::BC, n, vbuf(I1{}), dma);
-    f16x8 qf[T::KK];
-    load_q<T>(q + head, qrow, n, lane, negate_q, qf);
-    const Frag<T> fr(lane);
-
-    f32x16 oacc[T::DB];
-#pragma unroll
-    for (int db = 0; db < T::DB; ++db) oacc[db] = f32x16{};
-    float m_run = -INFINITY;
-    float l_run = 0.0F;
-
-    wait_vmem();
-    __syncthreads();
-    // Q has landed on every path (the compiler then never waits for it inside the loop).
-#pragma unroll
-    for (int kk = 0; kk < T::KK; ++kk) asm volatile("" ::"v"(qf[kk]));
-    f32x16 s[T::NB];
-    if (n_act > 0) qk_tile<T>(kbuf(I0{}), fr, qf, s);
-
-    FA_PHASE_DECL();
-    // The steady phases, compiled once per group so that every wait and refill of a wave is
-    // unconditional code (the compiler then tracks exactly which DMA has landed).
-    auto steady = [&](auto group) {
-        constexpr int G = decltype(group)::value;
-        // Requests of K_a into buffer a % 3 and V_b into buffer b % 3 (PA, PB: those buffers).
-        auto refill = [&](int a, auto pa, int b, auto pb) {
-            load_tile<T>(kh, a * T::BC, n, kbuf(pa), dma);
-            load_tile<T>(vh, b * T::BC, n, vbuf(pb), dma);
-        };
-        // The first phase ends only after every wave's QK_0 read of K buffer 0 (refilled below).
-        end_phase<false>();
-        if constexpr (G == 1) {  // group 1's M_{-1}: requests K_3 and V_2, then waits a phase
-            refill(3, I0{}, 2, I2{});
-            end_phase<false>();
-        }
-        auto tile = [&](int jj, auto r) {
-            FA_PHASE_T(ta);
-            constexpr int R = decltype(r)::value;  // jj % 3
-            using Rj = std::integral_constant<int, R>;
-            using Rj1 = std::integral_constant<int, (R + 1) % 3>;
-            using Rj2 = std::integral_constant<int, (R + 2) % 3>;
-            // softmax phase S_jj
-            if (FA_PP_MASKED_STEADY && g::tile_needs_mask(n, jj * T::BC, T::BC, qw, CAUSAL)) {
-                mask_tile<T, CAUSAL>(s, jj * T::BC, n, qrow, lane);
-            }
-            f16x8 kf[T::NB][T::KK];
-            f16x8 vf[T::NB][2][T::DB];
-            load_k_frags<T>(kbuf(Rj1{}), fr, kf);
-            load_v_frags<T>(vbuf(Rj{}), fr, vf);
-            f16x8 p[T::NB][2];
-            bool overflow;
-            softmax_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
-            // A wave issues in order, so 24 fragment reads in a row would stall its softmax
-            // behind the LDS queue; spread them over the VALU work instead.
-            sched_reads_valu<FA_PP_READS_PER, FA_PP_VALU_PER,
-                             (T::NB * T::KK + T::NB * 4 * T::DB) / FA_PP_READS_PER>();
-            // No branch here: the phase ends as soon as the softmax is issued, without waiting
-            // for its results. The overflow test is taken at the start of the matrix phase,
-            // before S is overwritten, when its flag has long been computed.
-            FA_PHASE_T(tb);
-            end_phase<G == 1>();
-            FA_PHASE_T(tc);
-            // matrix phase M_jj
-            if (__builtin_expect(overflow, 0)) {  // rare: exact softmax of this tile, new max,
-                float alpha;                       // rescaled O
-                bool rescale;
-                softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-                if (rescale) rescale_o<T>(oacc, alpha);
-            }
-            __builtin_amdgcn_s_setprio(FA_PP_PRIO);
-            matrix_phase<T>(kf, qf, vf, p, s, oacc, [&] {
-                if constexpr (G == 0) {
-                    refill(jj + 3, Rj{}, jj + 2, Rj2{});
-                } else {
-                    refill(jj + 4, Rj1{}, jj + 3, Rj{});
-                }
-            });
-            __builtin_amdgcn_s_setprio(0);
-            FA_PHASE_T(td);
-            end_phase<G == 0>();
-            FA_PHASE_T(te);
-            FA_PHASE_TILE(ta, tb, tc, td, te);
-        };
-        int jj = 0;
-        for (; jj + 3 <= n_steady; jj += 3) {
-            tile(jj, I0{});
-            tile(jj + 1, I1{});
-            tile(jj + 2, I2{});
-        }
-        if (jj < n_steady) tile(jj, I0{});
-        if (jj + 1 < n_steady) tile(jj + 1, I1{});
-        if constexpr (G == 0) end_phase<false>();  // group 0 waits out group 1's last matrix phase
-    };
-    if (n_steady > 0) {
-        if (grp == 0) {
-            steady(I0{});
-        } else {
-            steady(I1{});
-        }
-    }
-    char* kb[3];
-    char* vb[3];
-    kb[0] = k_lds0;
-    kb[1] = k_lds1;
-    kb[2] = k_lds2;
-    vb[0] = v_lds0;
-    vb[1] = v_lds1;
-    vb[2] = v_lds2;
-    general_tiles<T, CAUSAL, 3>(n_steady, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma,
-                                fr, qf, s, oacc, scale_log2, m_run, l_run);
-    store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
-               m_run, l_run, oacc);
-    FA_PHASE_STORE(wave, lane);
-    FA_CLOCK_END();
-}
-
 // ---- ping-pong on 16x16x32 MFMAs (D = 128 with 32-key tiles, D = 64 with 64-key tiles) --------
-// The schedule and buffer protocol of flash_fwd_pingpong, with the matrix work on
-// v_mfma_f32_16x16x32_f16 (two of half the FLOPs per 32x32x16). On MI355X, which runs this
+// The schedule and buffer protocol above, with the matrix work on v_mfma_f32_16x16x32_f16
+// (two of half the FLOPs per 32x32x16). On MI355X, which runs this
 // kernel at its power limit, a stream of 16x16x32 MFMAs on random fp16 data sustains about
 // 20 % more FLOPS than the same FLOPs in 32x32x16 MFMAs: the chip holds a higher clock.
 // Per wave (32 queries) and key tile: S^T in 16x16 blocks s[kb][qb] (key block kb =
@@ -1306,8 +981,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong(
 // fa::geom::pv16_key that the V^T operand reads. O^T in blocks oacc[db][qb] (features 16db..,
 // queries 16qb..). V tiles use the swizzle fa::geom::row_xor_m16; K tiles are stored so that
 // the K operand is read at the 32x32x16 path's conflict-free addresses (m16_kslot_row).
-// Fragment reads and softmax VALU of the softmax phase: N times {R reads, V VALU} (as
-// FA_PP_READS_PER / FA_PP_VALU_PER for flash_fwd_pingpong); R must divide the 24 reads.
+// Fragment reads and softmax VALU of the softmax phase: N times {R reads, V VALU}; R must
+// divide the 24 reads.
 #ifndef FA_PP16_READS_PER
 #define FA_PP16_READS_PER 8
 #endif
@@ -1605,7 +1280,10 @@ __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16
 }
 
 // O = acc / l as fp16 for the lane's two queries (if < n), and the natural-log LSE if lse_h is
-// not null. The lane holds features 16db + 4*(lane/16) + 0..3: one 8-byte store per db.
+// not null. The lane holds features 16db + 4*(lane/16) + 0..3 of each; lanes l and l ^ 16, which
+// hold the same query, trade half of them (pair_swap16) so that each lane writes 8 consecutive
+// features per 16-byte store: per pair of blocks (2e, 2e + 1) lane group g = lane / 16 stores
+// features 32e + 4g + 12 (g % 2) + 0..7, and the four groups cover 64 contiguous bytes.
 template <class T>
 __device__ __forceinline__ void store16(f16* oh, float* lse_h, int qw, int n, int lane,
                                         const float (&m_run)[M16<T>::QB],
@@ -1613,21 +1291,28 @@ __device__ __forceinline__ void store16(f16* oh, float* lse_h, int qw, int n, in
                                         const f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
     using G = M16<T>;
     float l_tot[G::QB];
+    f16x8 out[G::QB][G::DB / 2];
 #pragma unroll
-    for (int qb = 0; qb < G::QB; ++qb) l_tot[qb] = sum_xor32(sum_xor16(l_run[qb]));
+    for (int qb = 0; qb < G::QB; ++qb) {
+        l_tot[qb] = sum_xor32(sum_xor16(l_run[qb]));
+        const float inv = (l_tot[qb] > 0.0F) ? (1.0F / l_tot[qb]) : 0.0F;
+#pragma unroll
+        for (int e = 0; e < G::DB / 2; ++e) {
+            const f32x4& a = oacc[2 * e][qb];
+            const f32x4& b = oacc[2 * e + 1][qb];
+            out[qb][e] = pair_swap16(pack4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv),
+                                     pack4(b[0] * inv, b[1] * inv, b[2] * inv, b[3] * inv));
+        }
+    }
+    const int grp = lane >> 4;
 #pragma unroll
     for (int qb = 0; qb < G::QB; ++qb) {
         const int qrow = qw + g::st16_query(lane, qb);
         if (qrow >= n) continue;
-        const float inv = (l_tot[qb] > 0.0F) ? (1.0F / l_tot[qb]) : 0.0F;
         if (lse_h != nullptr && lane < 16) lse_h[qrow] = row_lse2(m_run[qb], l_tot[qb]) * kLn2;
-        f16* dst = oh + static_cast<size_t>(qrow) * G::D + 4 * (lane >> 4);
+        f16* dst = oh + static_cast<size_t>(qrow) * G::D + 4 * grp + 12 * (grp & 1);
 #pragma unroll
-        for (int db = 0; db < G::DB; ++db) {
-            const f32x4& a = oacc[db][qb];
-            *reinterpret_cast<f16x4*>(dst + 16 * db) =
-                pack4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-        }
+        for (int e = 0; e < G::DB / 2; ++e) *reinterpret_cast<f16x8*>(dst + 32 * e) = out[qb][e];
     }
 }
 
@@ -1723,7 +1408,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
-    FA_CLOCK_BEGIN();
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1756,6 +1440,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const f16* kh = k + head + static_cast<size_t>(key0) * T::D;
     const f16* vh = v + head + static_cast<size_t>(key0) * T::D;
     const int n_tiles = range.count;
+    // DMA bound: the keys this workgroup visits (its split range, or up to its causal diagonal).
+    // The prefetches that run past the last tile still issue, so every wave's vmcnt sequence is
+    // unchanged, but they read zeros instead of keys of the next range or right of the diagonal.
+    const int nk_load = min(nk, n_tiles * T::BC);
     // (a split can start right of all of this wave's queries: no active tile then)
     const int n_act = (SPLIT && CAUSAL && qk + 31 < 0)
                           ? 0
@@ -1781,11 +1469,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 
     const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
     const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
-    load_tile<T>(kh, 0, nk, kbuf(I0{}), dma_k);
-    load_tile<T>(vh, 0, nk, vbuf(I0{}), dma);
-    load_tile<T>(kh, T::BC, nk, kbuf(I1{}), dma_k);
-    load_tile<T>(kh, 2 * T::BC, nk, kbuf(I2{}), dma_k);
-    load_tile<T>(vh, T::BC, nk, vbuf(I1{}), dma);
+    load_tile<T>(kh, 0, nk_load, kbuf(I0{}), dma_k);
+    load_tile<T>(vh, 0, nk_load, vbuf(I0{}), dma);
+    load_tile<T>(kh, T::BC, nk_load, kbuf(I1{}), dma_k);
+    load_tile<T>(kh, 2 * T::BC, nk_load, kbuf(I2{}), dma_k);
+    load_tile<T>(vh, T::BC, nk_load, vbuf(I1{}), dma);
     f16x8 qf[G::QB][G::DC];
     load_q16<T>(q + head, qw, n, lane, negate_q, qf);
     const Frag16<T> fr(lane);
@@ -1804,15 +1492,21 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     for (int qb = 0; qb < G::QB; ++qb)
 #pragma unroll
         for (int dc = 0; dc < G::DC; ++dc) asm volatile("" ::"v"(qf[qb][dc]));
+    // A wave with no active tile (entirely past the end of the sequence, or left of a split's
+    // keys) never computes S, but the non-causal steady loop still runs its softmax on masked
+    // scores: start from zeros so that it reads defined values.
     f32x4 s[G::KB][G::QB];
+#pragma unroll
+    for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = f32x4{};
     if (n_act > 0) qk16<T>(kbuf(I0{}), fr, qf, s);
 
-    FA_PHASE_DECL();
     auto steady = [&](auto group) {
         constexpr int G = decltype(group)::value;
         auto refill = [&](int a, auto pa, int b, auto pb) {
-            load_tile<T>(kh, a * T::BC, nk, kbuf(pa), dma_k);
-            load_tile<T>(vh, b * T::BC, nk, vbuf(pb), dma);
+            load_tile<T>(kh, a * T::BC, nk_load, kbuf(pa), dma_k);
+            load_tile<T>(vh, b * T::BC, nk_load, vbuf(pb), dma);
         };
         end_phase<false>();
         if constexpr (G == 1) {
@@ -1820,7 +1514,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             end_phase<false>();
         }
         auto tile = [&](int jj, auto r) {
-            FA_PHASE_T(ta);
             constexpr int R = decltype(r)::value;
             using Rj = std::integral_constant<int, R>;
             using Rj1 = std::integral_constant<int, (R + 1) % 3>;
@@ -1838,9 +1531,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
             static_assert(G::READS % FA_PP16_READS_PER == 0, "FA_PP16_READS_PER must divide 24");
             sched_reads_valu<FA_PP16_READS_PER, FA_PP16_VALU_PER, G::READS / FA_PP16_READS_PER>();
-            FA_PHASE_T(tb);
             end_phase<G == 1>();
-            FA_PHASE_T(tc);
             // matrix phase M_jj
             if (__builtin_expect(overflow, 0)) {
                 float alpha[G::QB];
@@ -1857,10 +1548,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 }
             });
             __builtin_amdgcn_s_setprio(0);
-            FA_PHASE_T(td);
             end_phase<G == 0>();
-            FA_PHASE_T(te);
-            FA_PHASE_TILE(ta, tb, tc, td, te);
         };
         int jj = 0;
         for (; jj + 3 <= n_busy; jj += 3) {
@@ -1880,11 +1568,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 const int r = t % 3;
                 end_phase<G == 1>();
                 if constexpr (G == 0) {
-                    load_tile<T>(kh, (t + 3) * T::BC, nk, kb_at(r), dma_k);
-                    load_tile<T>(vh, (t + 2) * T::BC, nk, vb_at((r + 2) % 3), dma);
+                    load_tile<T>(kh, (t + 3) * T::BC, nk_load, kb_at(r), dma_k);
+                    load_tile<T>(vh, (t + 2) * T::BC, nk_load, vb_at((r + 2) % 3), dma);
                 } else {
-                    load_tile<T>(kh, (t + 4) * T::BC, nk, kb_at((r + 1) % 3), dma_k);
-                    load_tile<T>(vh, (t + 3) * T::BC, nk, vb_at(r), dma);
+                    load_tile<T>(kh, (t + 4) * T::BC, nk_load, kb_at((r + 1) % 3), dma_k);
+                    load_tile<T>(vh, (t + 3) * T::BC, nk_load, vb_at(r), dma);
                 }
                 end_phase<G == 0>();
             }
@@ -1916,114 +1604,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
                    m_run, l_run, oacc);
     }
-    FA_PHASE_STORE(wave, lane);
-    FA_CLOCK_END();
-}
-
-// ---- simple schedule on 16x16x32 MFMAs ---------------------------------------------------------
-// flash_fwd_kernel's schedule (barrier, prefetch of tile j+1, QK^T, exact softmax and P.V of tile
-// j) with the 16x16x32 layouts of flash_fwd_pingpong16. Fragments are read from LDS right before
-// the MFMAs that use them, so that the d=64 tile keeps four waves per SIMD.
-template <class T>
-__device__ __forceinline__ void qk16_inline(const char* kl, const Frag16<T>& fr,
-                                            const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
-                                            f32x4 (&s)[M16<T>::KB][M16<T>::QB]) {
-    using G = M16<T>;
-#pragma unroll
-    for (int kb = 0; kb < G::KB; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = f32x4{};
-#pragma unroll
-    for (int dc = 0; dc < G::DC; ++dc)
-#pragma unroll
-        for (int kb = 0; kb < G::KB; ++kb) {
-            const f16x8 a = *reinterpret_cast<const f16x8*>(kl + fr.koff[kb][dc]);
-#pragma unroll
-            for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = mfma16(a, qf[qb][dc], s[kb][qb]);
-        }
-}
-
-template <class T>
-__device__ __forceinline__ void pv16_inline(const char* vl, const Frag16<T>& fr,
-                                            const f16x8 (&p)[M16<T>::QB][M16<T>::KS],
-                                            f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
-    using G = M16<T>;
-#pragma unroll
-    for (int t = 0; t < G::KS; ++t)
-#pragma unroll
-        for (int db = 0; db < G::DB; ++db) {
-            const char* base = vl + fr.voff[db] + 32 * t * G::ROW;
-            const f16x4 lo = lds_read_tr16(base);
-            const f16x4 up = lds_read_tr16(base + 8 * G::ROW);
-            const f16x8 a = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-#pragma unroll
-            for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = mfma16(a, p[qb][t], oacc[db][qb]);
-        }
-}
-
-template <class T, bool CAUSAL>
-__global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
-    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
-    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
-    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
-    float* /*lse_part*/) {
-    using G = M16<T>;
-    static_assert(T::NBUF == 2, "double-buffered K and V");
-    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
-    FA_CLOCK_BEGIN();
-
-    const int lane = threadIdx.x & 63;
-    const int wave = wave_uniform(threadIdx.x >> 6);
-    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
-    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
-    const f16* kh = k + head;
-    const f16* vh = v + head;
-    const int q0 = w.qb * T::BR;
-    const int qw = q0 + wave * 32;  // first query of this wave
-    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-
-    // LDS: [K0 | K1 | V0 | V1]; buffer b of K at b*TILE_BYTES, of V at (2+b)*TILE_BYTES.
-    auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
-    auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
-
-    const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
-    const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
-    load_tile<T>(kh, 0, n, kbuf(0), dma_k);
-    load_tile<T>(vh, 0, n, vbuf(0), dma);
-    f16x8 qf[G::QB][G::DC];
-    load_q16<T>(q + head, qw, n, lane, negate_q, qf);
-    const Frag16<T> fr(lane);
-
-    f32x4 oacc[G::DB][G::QB];
-#pragma unroll
-    for (int db = 0; db < G::DB; ++db)
-#pragma unroll
-        for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = f32x4{};
-    float m_run[G::QB] = {-INFINITY, -INFINITY};
-    float l_run[G::QB] = {0.0F, 0.0F};
-
-    for (int j = 0; j < n_tiles; ++j) {
-        wait_vmem();
-        __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
-        if (j + 1 < n_tiles) {
-            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf((j + 1) & 1), dma_k);
-            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), dma);
-        }
-        const int kt = j * T::BC;
-        if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) continue;  // wave-uniform
-        f32x4 s[G::KB][G::QB];
-        qk16_inline<T>(kbuf(j & 1), fr, qf, s);
-        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask16<T, CAUSAL>(s, kt, n, qw, lane);
-        f16x8 p[G::QB][G::KS];
-        float alpha[G::QB];
-        bool rescale;
-        softmax16_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale16<T>(oacc, alpha);
-        pv16_inline<T>(vbuf(j & 1), fr, p, oacc);
-    }
-    store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane, m_run,
-               l_run, oacc);
-    FA_CLOCK_END();
 }
 
 // ---- tile table -------------------------------------------------------------------------------
@@ -2221,12 +1801,8 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
         } else {
             fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
         }
-    } else if constexpr (T::SCHED == PINGPONG) {
-        fn = reinterpret_cast<const void*>(&flash_fwd_pingpong<T, CAUSAL>);
     } else if constexpr (T::SCHED == PINGPONG16) {
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL>);
-    } else if constexpr (T::SCHED == SIMPLE16) {
-        fn = reinterpret_cast<const void*>(&flash_fwd_simple16<T, CAUSAL>);
     } else if constexpr (T::SCHED == KSPLIT) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
     } else if constexpr (T::SCHED == PIPE) {
@@ -2336,11 +1912,26 @@ SplitPlan split_plan(const fa_params& p, int requested) {
     return sp;
 }
 
+// Whether fa_flash_fwd leaves most of the GPU idle on these params and the automatic split-KV
+// plan is expected to be faster (measured on MI355X over few-head shapes at d = 64 and 128:
+// the split path wins from N = 4096 on grids of fewer 8-wave workgroups than CUs, except
+// causal d = 64, whose partial pass keeps the 4-wave simple tile and loses by a few percent).
+#ifndef FA_SPLITKV_MIN_N
+#define FA_SPLITKV_MIN_N 4096
+#endif
+bool splitkv_preferred(const fa_params& p) {
+    if (p.variant == FA_VARIANT_BASELINE || p.seqlen < FA_SPLITKV_MIN_N) return false;
+    if (p.head_dim == 64 && p.causal) return false;
+    const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
+    if (bh * ((static_cast<int64_t>(p.seqlen) + 255) / 256) >= FA_SMALL_GRID_WGS) return false;
+    return split_plan(p, 0).n_splits >= 2;
+}
+
 template <int D>
 int combine(const fa_params& p, const SplitPlan& sp, const float* o_part, const float* lse_part,
             float* lse, hipStream_t stream) {
     const int64_t rows = static_cast<int64_t>(p.batch) * p.heads * p.seqlen;
-    constexpr int ROWS_PER_BLOCK = 256 / (D / 4);
+    constexpr int ROWS_PER_BLOCK = CombineGeom<D>::ROWS;
     const auto blocks = static_cast<unsigned>((rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK);
     auto* op = static_cast<f16*>(p.o);
     int n = p.seqlen, bh = p.batch * p.heads, ns = sp.n_splits, tps = sp.tiles_per_split;
@@ -2381,19 +1972,6 @@ bool tile_of(int head_dim, bool causal, int variant, int seqlen, int64_t bh, fa_
 }  // namespace fa
 
 extern "C" {
-
-#if FA_CLOCK_PROBE
-// Copies the per-workgroup records of the last launch into `host` (65536 x 4 entries: shader
-// cycles, 10 ns ticks, start tick, XCC_ID << 32 | HW_ID). Exists only in the clock-probe build.
-int fa_probe_clock_fetch(unsigned long long* host) {
-    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fa_clock), sizeof(g_fa_clock)));
-}
-
-// Copies the ping-pong phase sums of the last launch (8192 workgroups x 8 waves x 6) to `host`.
-int fa_probe_phase_fetch(unsigned long long* host) {
-    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_fa_phase), sizeof(g_fa_phase)));
-}
-#endif
 
 const char* fa_last_error(void) { return fa::g_last_error.c_str(); }
 
@@ -2498,7 +2076,7 @@ int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info
     if (num_splits < 0) return fa::fail(FA_EINVAL, "fa_splitkv_plan: num_splits must be >= 0");
     const fa::SplitPlan sp = fa::split_plan(p, num_splits);
     *out = fa_splitkv_info{sp.n_splits, sp.tiles_per_split, sp.block_q, sp.block_k,
-                           sp.workspace_bytes};
+                           sp.workspace_bytes, fa::splitkv_preferred(p) ? 1 : 0, 0};
     return FA_OK;
 }
 

@@ -11,10 +11,9 @@ slot: one row of the tile table in csrc/flash_fwd.hip, named after its macro (se
       opt_d64_causal_short, opt_d64_causal, opt_d64_causal_long, opt_d128,
       opt_d128_causal_short, opt_d128_causal, base_d64, base_d128
 cand: "BC,NW,LAZY,SCHED" -- keys per tile, query waves per workgroup (BR = 32 * NW), lazy
-      rescale (true/false) and schedule (SIMPLE, PIPE, PINGPONG, KSPLIT, which runs two waves
-      per query wave, or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128,
-      BC=64 at D=64; SIMPLE16 the simple schedule on those layouts), e.g. 32,8,true,PINGPONG16.
-      Without candidates a default list for the slot is used.
+      rescale (true/false) and schedule (SIMPLE, PIPE, KSPLIT, which runs two waves per query
+      wave, or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128, BC=64 at
+      D=64), e.g. 32,8,true,PINGPONG16. Without candidates a default list for the slot is used.
 
 `build` compiles csrc/flash_fwd.hip once per candidate with the slot's macro overridden, into
 dev/_tune/<slot>/<cand>.so (candidates the tile checks reject fail to compile and are reported
@@ -22,8 +21,12 @@ as such), with the size thresholds of the table pinned so that the slot's row ru
 and B*H. `run` times every built library with dev/fa_dev on the
 FlashAttention-2 paper shapes (B = 16384 / N, H = 2048 / d; --bh fixes B and H instead),
 which also checks a sample of output rows; --dev-args passes input options to fa_dev. Each
-cell is the best of `reps` medians (TFLOPS), and the table is printed and written as CSV. The library in fa/ is never touched: copy a winning candidate into the tile
-table by hand.
+cell is the best of `reps` medians (TFLOPS), and the table is printed and written as CSV. A
+candidate whose output check fails (fa_dev exit 1) is recorded as FAIL and the sweep goes on;
+a child killed by a signal or exiting 2 (a HIP runtime error, e.g. a memory fault) stops the
+whole sweep with a non-zero status, so no further kernel is launched after a possible GPU
+fault. The library in fa/ is never touched: copy a winning candidate into the tile table by
+hand.
 Counterpart of the reference's bench/tune.sh:49-71 (which rewrites the `using` line of its
 tile table, rebuilds fa_dev and runs it on the same shapes).
 """
@@ -72,13 +75,10 @@ SLOTS = {
     "base_d128": ("FA_BASE_D128", "base", 128, 0, []),
 }
 DEFAULT_CANDS = {
-    64: ["32,4,true,PIPE", "64,4,true,PIPE", "64,8,true,PINGPONG16", "64,8,true,PINGPONG",
-         "32,4,true,SIMPLE", "64,8,true,SIMPLE16",
+    64: ["32,4,true,PIPE", "64,4,true,PIPE", "64,8,true,PINGPONG16", "32,4,true,SIMPLE",
          "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "64,2,true,KSPLIT",
          "32,2,true,KSPLIT"],
-    128: ["32,8,true,PINGPONG16", "32,8,true,PINGPONG", "32,8,true,PIPE", "32,4,true,SIMPLE",
-          "32,4,true,SIMPLE16",
-          "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "32,2,true,KSPLIT",
+    128: ["32,8,true,PINGPONG16", "32,8,true,PIPE", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "32,2,true,KSPLIT",
           "32,4,true,KSPLIT"],
 }
 
@@ -138,6 +138,12 @@ def run(slot: str, ns: list[int], reps: int, csv_path: Path | None,
                 args = [str(fa_dev), str(b), str(h), str(n), str(d), str(causal), "30", variant,
                         "--lib", str(lib), "--json", *shlex.split(dev_args)]
                 res = subprocess.run(args, capture_output=True, text=True, timeout=300)
+                if res.returncode < 0 or res.returncode == 2:
+                    # killed by a signal (e.g. a memory-fault abort) or a HIP runtime error:
+                    # the GPU may be in a bad state, launch nothing more
+                    print(f"  {cand} N={n}: fa_dev ended with rc={res.returncode}; stopping the "
+                          f"sweep\n{res.stderr.strip()[-2000:]}", file=sys.stderr, flush=True)
+                    return 3
                 line = res.stdout.strip().splitlines()[0] if res.stdout.strip() else ""
                 if res.returncode != 0 or not line.startswith("{"):
                     best = "FAIL"

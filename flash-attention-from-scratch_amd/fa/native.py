@@ -55,6 +55,8 @@ class FaSplitKvInfo(ctypes.Structure):
         ("block_q", ctypes.c_int32),
         ("block_k", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_uint64),
+        ("preferred", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -9,8 +9,6 @@ Targets (outputs are git-ignored; they travel to the GPU box with the source tre
   blocks  tests/blocks/libfa_blocks.so   building-block kernels for the GPU unit tests
   oracle  oracle/liboracle_fp64.so       the C fp64 oracle (gcc), test infrastructure only
   geom    tests/geometry/libfa_geom.so   host build of the tile geometry, for the CPU tests
-  probe   fa/libfa_probe.so, fa/libfa_hip_clock.so   measurement only (python -m fa.probe):
-          MFMA power-ceiling probes, and the kernels with per-workgroup clock recording
   dev     dev/fa_dev             standalone C++ driver (no Python) over the C ABI, for
           rocprofv3 counter runs and tile tuning (dev/counters.sh, dev/tune.py)
 
@@ -166,15 +164,6 @@ def build_geom() -> Path:
     return out
 
 
-def build_probe() -> list[Path]:
-    out = FA / "libfa_probe.so"
-    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{CSRC}", str(CSRC / "fa_probe.hip"), "-o", str(out)])
-    clock = FA / "libfa_hip_clock.so"
-    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", "-DFA_CLOCK_PROBE=1",
-          str(CSRC / "flash_fwd.hip"), "-o", str(clock)])
-    return [out, clock]
-
-
 def build_dev() -> Path:
     src = PKG / "dev" / "fa_dev.cpp"
     out = src.parent / "fa_dev"
@@ -183,8 +172,8 @@ def build_dev() -> Path:
 
 
 TARGETS = {"lib": build_lib, "ext": build_ext, "blocks": build_blocks, "oracle": build_oracle,
-           "geom": build_geom, "probe": build_probe, "dev": build_dev}
-ALL = ("lib", "ext", "blocks", "oracle", "geom", "probe", "dev")
+           "geom": build_geom, "dev": build_dev}
+ALL = ("lib", "ext", "blocks", "oracle", "geom", "dev")
 
 
 def build_all() -> None:

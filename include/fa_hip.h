@@ -82,12 +82,14 @@ int fa_flash_fwd_lse(const fa_params* params, float* lse, void* stream);
  * long sequences): the key tiles of every query block are cut into ranges, one workgroup per
  * (query block, range) writes a partial O and LSE per row to the caller's workspace, and a
  * second kernel merges them by their LSEs. Same results as fa_flash_fwd within fp32 rounding
- * of the merge (not bitwise). No counterpart in the reference.
+ * of the merge (not bitwise). No counterpart in the reference (its docs list split-KV as not
+ * done: docs/optimizations.md:372-373).
  * fa_splitkv_plan reports the ranges and the workspace size for num_splits (0 = automatic:
- * 256 to 1024 workgroups with work, by head_dim and causal); host-only. fa_flash_fwd_splitkv runs it: lse may be
- * NULL; workspace must be 16-byte aligned and hold at least workspace_bytes of the plan for the
- * same params and num_splits. Two launches on `stream`; allocates nothing. The variant field
- * is checked but every variant runs the same split tile. */
+ * 256 to 1024 workgroups with work, by head_dim and causal), and whether the split path is the
+ * faster one for these params; host-only. fa_flash_fwd_splitkv runs it: lse may be NULL;
+ * workspace must be 16-byte aligned and hold at least workspace_bytes of the plan for the same
+ * params and num_splits. Two launches on `stream`; allocates nothing. The variant field is
+ * checked but every variant runs the same split tile. */
 typedef struct fa_splitkv_info {
     int32_t num_splits;       /* key ranges per query block (ranges past a causal block's last
                                  key tile are skipped)                                        */
@@ -95,6 +97,12 @@ typedef struct fa_splitkv_info {
     int32_t block_q;          /* query rows per workgroup of the partial pass                 */
     int32_t block_k;          /* keys per tile                                                */
     uint64_t workspace_bytes; /* num_splits * B * H * N * (D + 1) * 4                         */
+    int32_t preferred;        /* 1 if the automatic split-KV plan is expected to beat
+                                 fa_flash_fwd on these params (variant not baseline, a grid
+                                 that leaves most CUs idle, N >= 4096, not causal at D = 64),
+                                 else 0; independent of num_splits. The PyTorch binding's
+                                 forward takes the split path exactly when it is 1.           */
+    int32_t reserved;         /* 0                                                            */
 } fa_splitkv_info;
 int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info* out);
 int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits,

@@ -90,6 +90,17 @@ __global__ void k_xor16(const float* in, float* out_max, float* out_sum) {
     out_sum[l] = sum_xor16(in[l]);
 }
 
+// pair_swap16 / pair_swap32 (the 16-byte output stores): lane l passes a = in[8l .. 8l+3] and
+// b = in[8l+4 .. 8l+7] (as fp16) and writes the 8 halves it gets back to out[8l .. 8l+7].
+__global__ void k_pair_swap(const uint16_t* in, uint16_t* out, int dist) {
+    const int l = threadIdx.x;
+    const u16x8 x = *reinterpret_cast<const u16x8*>(in + 8 * l);
+    const f16x4 a = __builtin_bit_cast(f16x4, u16x4{x[0], x[1], x[2], x[3]});
+    const f16x4 b = __builtin_bit_cast(f16x4, u16x4{x[4], x[5], x[6], x[7]});
+    const u16x8 r = bits8(dist == 16 ? pair_swap16(a, b) : pair_swap32(a, b));
+    *reinterpret_cast<u16x8*>(out + 8 * l) = r;
+}
+
 __global__ void k_exp2(const float* x, float* y, int n) {
     for (int i = threadIdx.x; i < n; i += 64) y[i] = exp2_fast(x[i]);
 }
@@ -235,6 +246,16 @@ int fab_xor16(const float* in, float* out_max, float* out_sum) {
     FAB_TRY(hipDeviceSynchronize());
     FAB_TRY(to_host(out_max, dm, 64));
     return to_host(out_sum, ds, 64);
+}
+
+int fab_pair_swap(const uint16_t* in, uint16_t* out, int dist) {
+    DevBuf<uint16_t> di(512), dout(512);
+    FAB_TRY(to_dev(di, in, 512));
+    FAB_TRY(dout.err);
+    hipLaunchKernelGGL(k_pair_swap, dim3(1), dim3(64), 0, 0, di.p, dout.p, dist);
+    FAB_TRY(hipGetLastError());
+    FAB_TRY(hipDeviceSynchronize());
+    return to_host(out, dout, 512);
 }
 
 int fab_exp2(const float* x, float* y, int n) {

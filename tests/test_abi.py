@@ -229,3 +229,41 @@ def test_splitkv_entry_rejects_bad_workspace():
     with pytest.raises(ValueError, match="num_splits"):
         native.splitkv_plan(p, -2)
 
+
+
+@pytest.mark.parametrize("b,h,n,d,causal,variant,want", [
+    # few heads of long sequences: the split-KV path
+    (1, 1, 16384, 128, False, "opt", 1), (1, 2, 16384, 128, True, "opt", 1),
+    (1, 1, 32768, 128, True, "fp16acc", 1), (1, 2, 4096, 128, True, "opt", 1),
+    (1, 4, 8192, 64, False, "opt", 1),
+    # one step past each boundary of the rule
+    (1, 2, 4095, 128, True, "opt", 0),         # N below 4096
+    (1, 4, 8192, 64, True, "opt", 0),          # causal d = 64
+    (1, 16, 4096, 128, False, "opt", 0),       # 256 workgroups of 8 waves fill the GPU
+    (1, 15, 4096, 128, False, "opt", 1),       # 240 do not
+    (1, 2, 16384, 128, False, "baseline", 0),  # the baseline build is never re-routed
+    (2, 8, 1000, 64, True, "opt", 0), (16, 32, 2048, 64, True, "opt", 0),
+    (1, 16, 16384, 128, False, "opt", 0),      # the headline shape
+])
+def test_splitkv_preferred_flag(b, h, n, d, causal, variant, want):
+    p = native.make_params(**{**GOOD, "batch": b, "heads": h, "seqlen": n, "head_dim": d,
+                              "causal": causal, "variant": variant})
+    for req in (0, 3):   # independent of the requested split count
+        plan = native.splitkv_plan(p, req)
+        assert plan["preferred"] == want and plan["reserved"] == 0
+
+
+def test_splitkv_info_layout_matches_header(tmp_path):
+    src = tmp_path / "info.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "fa_hip.h"\n'
+        "int main(void){printf(\"%zu %zu %zu\\n\", sizeof(fa_splitkv_info),"
+        " offsetof(fa_splitkv_info, workspace_bytes), offsetof(fa_splitkv_info, preferred));"
+        " return 0;}\n")
+    exe = tmp_path / "info"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{REPO / 'include'}", str(src),
+                    "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    S = native.FaSplitKvInfo
+    assert got == [ctypes.sizeof(S), S.workspace_bytes.offset, S.preferred.offset]

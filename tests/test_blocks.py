@@ -150,3 +150,24 @@ def test_sum8_f16_accumulates_in_fp32(blk):
     _ok(blk.fab_sum8(_ptr(x.view(np.uint16)), _ptr(y), ctypes.c_int(1000)))
     want = x.astype(np.float64).sum(axis=1)
     np.testing.assert_allclose(y, want, rtol=2e-7 * 8, atol=0)
+
+
+@pytest.mark.parametrize("dist", [16, 32])
+def test_pair_swap_lane_layout(blk, dist):
+    """pair_swap16 / pair_swap32: lane l of the lower row of each pair (l % (2 dist) < dist)
+    gets {a[l], a[l + dist]}, lane l of the upper row {b[l - dist], b[l]} -- the exchange that
+    lets each lane of a pair store 8 consecutive output features with one 16-byte store."""
+    vals = np.arange(512, dtype=np.float16)          # lane l: a = 8l .. 8l+3, b = 8l+4 .. 8l+7
+    out = np.zeros(512, dtype=np.uint16)
+    _ok(blk.fab_pair_swap(_ptr(vals.view(np.uint16)), _ptr(out), dist))
+    got = out.view(np.float16).astype(np.int64).reshape(64, 8)
+    a = np.arange(512).reshape(64, 8)[:, :4]
+    b = np.arange(512).reshape(64, 8)[:, 4:]
+    want = np.zeros((64, 8), dtype=np.int64)
+    for lane in range(64):
+        p = lane ^ dist
+        if lane % (2 * dist) < dist:
+            want[lane] = np.concatenate([a[lane], a[p]])
+        else:
+            want[lane] = np.concatenate([b[p], b[lane]])
+    np.testing.assert_array_equal(got, want)

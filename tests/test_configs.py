@@ -1,9 +1,10 @@
 """GPU: the five benchmark configurations at full size, against the oracle.
 
-Small configs (1, 3) are checked on every row with the fp32 oracle. For the large ones the
-oracle runs on sampled (batch, head) slices (fp32, whole slice) and sampled rows (fp64 C brute
-force), and size-independent properties cover the rest: the q = 0 closed form on every row
-(O = mean(V), or prefix means when causal), finiteness and bitwise determinism.
+Every (batch, head) slice of every configuration is compared with the fp32 oracle (whole
+slices, one at a time on the host: about 15 s of CPU work for cfg2, cfg4 and cfg5 together),
+and for the large ones selected rows of a few slices also with the fp64 C brute force.
+Size-independent properties add the q = 0 closed form on every row (O = mean(V), or prefix
+means when causal), finiteness and bitwise determinism.
 Tolerance |out - ref| <= 2e-3 + 1e-2 |ref| throughout.
 """
 
@@ -30,7 +31,7 @@ def _close(out, ref):
 
 CASES = [("cfg1", False), ("cfg2", False), ("cfg2", True), ("cfg3", True), ("cfg4", False),
          ("cfg4", True), ("cfg5", True)]
-SAMPLE_SLICES = {"cfg2": [0, 37, 63], "cfg4": [0, 15], "cfg5": [0, 200, 511]}
+FP64_SLICES = {"cfg2": [0, 37, 63], "cfg4": [0, 15], "cfg5": [0, 200, 511]}
 
 
 @pytest.mark.parametrize("name,causal", CASES)
@@ -44,15 +45,12 @@ def test_config_matches_oracle(name, causal):
     out = fa.forward(q, k, v, causal=causal)
     assert torch.isfinite(out).all()
     b, h, n, d = q.shape
-    if name not in SAMPLE_SLICES:
-        _close(out, orc.attention_fp32(q, k, v, causal=causal))
-        return
-    of = out.view(b * h, n, d)
-    qf, kf, vf = (t.view(b * h, 1, n, d) for t in (q, k, v))
-    for bh in SAMPLE_SLICES[name]:
-        if n <= 4096:
-            _close(of[bh], orc.attention_fp32(qf[bh:bh + 1], kf[bh:bh + 1], vf[bh:bh + 1],
-                                              causal=causal)[0, 0])
+    of = out.view(b * h, n, d).cpu()
+    qc, kc, vc = (t.cpu().view(b * h, 1, n, d) for t in (q, k, v))
+    for bh in range(b * h):
+        ref = orc.attention_fp32(qc[bh:bh + 1], kc[bh:bh + 1], vc[bh:bh + 1], causal=causal)
+        _close(of[bh], ref[0, 0])
+    for bh in FP64_SLICES.get(name, []):
         rows = sorted({0, 1, 31, 32, 127, 128, n // 3, n // 2 + 17, n - 129, n - 2, n - 1})
         ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, causal, bh, rows))
         _close(of[bh, rows], ref)

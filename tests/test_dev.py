@@ -48,7 +48,7 @@ def _write_csv(path: Path, header: list[str], rows: list[list]):
         w.writerows(rows)
 
 
-@pytest.mark.parametrize("kname, fpm, shape", [("_ZN2fa18flash_fwd_pingpongE", 32768, "32x32x16"),
+@pytest.mark.parametrize("kname, fpm, shape", [("_ZN2fa16flash_fwd_kernelE", 32768, "32x32x16"),
                                                ("_ZN2fa20flash_fwd_pingpong16E", 16384, "16x16x32")])
 def test_counters_summary(tmp_path, kname, fpm, shape):
     """Two dispatches of a kernel: the first (the checked launch) is dropped, and the derived

@@ -19,7 +19,7 @@ import pytest
 RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" / "fa" / \
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
-SIMPLE, PIPE, PINGPONG, KSPLIT, PINGPONG16 = 0, 1, 2, 3, 4
+SIMPLE, PIPE, KSPLIT, PINGPONG16 = 0, 1, 3, 4
 
 
 def _load():
@@ -32,7 +32,7 @@ def _min_occupancy(name: str) -> int:
     if "flash_fwd_combine" in name:
         return 4
     d, bc, nw, _lazy, sched = (int(x) for x in TILE.search(name).groups())
-    if "flash_fwd_pingpong" in name:  # flash_fwd_pingpong and flash_fwd_pingpong16
+    if "flash_fwd_pingpong16" in name:
         return 2                      # waves w and w+4 share a SIMD
     if "flash_fwd_ksplit" in name:
         return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
@@ -42,12 +42,18 @@ def _min_occupancy(name: str) -> int:
     return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
 
 
+def _family(mangled: str) -> str:
+    """Kernel function name of a mangled symbol (_ZN2fa12_GLOBAL__N_1<len><name>I...)."""
+    m = re.search(r"_GLOBAL__N_1(\d+)", mangled)
+    assert m, mangled
+    start = m.end()
+    return mangled[start:start + int(m.group(1))]
+
+
 def test_every_kernel_is_recorded():
-    res = _load()
-    families = {k.split("INS0_")[0].split("ILi")[0] for k in res}
-    for f in ("flash_fwd_kernel", "flash_fwd_pingpong", "flash_fwd_pipelined", "flash_fwd_ksplit",
-              "flash_fwd_combine"):
-        assert any(f in x for x in families), f
+    families = {_family(k) for k in _load()}
+    assert families == {"flash_fwd_kernel", "flash_fwd_pingpong16", "flash_fwd_pipelined",
+                        "flash_fwd_ksplit", "flash_fwd_combine"}, families
 
 
 def test_no_kernel_spills_to_scratch():
