@@ -37,6 +37,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 #include <utility>
@@ -44,6 +45,10 @@
 #include "fa_device.h"
 #include "fa_geometry.h"
 #include "fa_hip.h"
+
+// Workspace of fa_flash_fwd_splitkv_static (see static_scratch below): FA_STATIC_SCRATCH_BYTES
+// (fa_hip.h) per GPU.
+static __device__ __align__(256) float scratch[FA_STATIC_SCRATCH_BYTES / sizeof(float)];
 
 namespace fa {
 namespace {
@@ -1961,6 +1966,43 @@ int splitkv(const fa_params& p, float* lse, const SplitPlan& sp, void* workspace
     return combine<T::D>(p, sp, o_part, lse_part, lse, stream);
 }
 
+// ---- static scratch of the allocation-free split-KV entry point -------------------------------
+// fa_flash_fwd_splitkv_static takes its partial-O / LSE workspace from `scratch`, a file-scope
+// device array that every GPU the library runs on holds until the process ends. In host code
+// the array's name only stands for the symbol; its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and kept in g_scratch_ptr. The partial pass
+// writes every (range, row) entry the combine kernel reads, so nothing needs clearing between
+// calls; calls that overlap on one GPU share the array and race.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int static_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        return fail(FA_EHIP, std::string("flash_fwd_splitkv_static: hipGetDevice failed: ") +
+                                 hipGetErrorString(e));
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        return fail(FA_EHIP, "flash_fwd_splitkv_static: device index " + std::to_string(dev) +
+                                 " beyond the " + std::to_string(kMaxDevices) + " supported");
+    }
+    const std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            return fail(FA_EHIP, std::string("flash_fwd_splitkv_static: hipGetSymbolAddress of "
+                                             "the scratch array failed: ") +
+                                     hipGetErrorString(e));
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FA_OK;
+}
+
 bool tile_of(int head_dim, bool causal, int variant, int seqlen, int64_t bh, fa_tile_info* out) {
     if (head_dim != 64 && head_dim != 128) return false;
     *out = with_row(tile_id(head_dim, causal, variant, seqlen, bh),
@@ -2080,21 +2122,40 @@ int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info
     return FA_OK;
 }
 
+// Checks shared by the two split-KV entry points (before any HIP call); the plan on success.
+static int splitkv_checks(const fa_params* params, float* lse, int32_t num_splits, const char* who,
+                          fa::SplitPlan* plan) {
+    const std::string w = std::string(who) + ": ";
+    const int rc = validate(params, who);
+    if (rc != FA_OK) return rc;
+    const fa_params& p = *params;
+    if (num_splits < 0) return fa::fail(FA_EINVAL, w + "num_splits must be >= 0");
+    if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3U) != 0) {
+        return fa::fail(FA_EINVAL, w + "lse must be 4-byte aligned");
+    }
+    *plan = fa::split_plan(p, num_splits);
+    if (static_cast<int64_t>(p.batch) * p.heads * fa::g::ceil_div(p.seqlen, plan->block_q) *
+            plan->n_splits > INT32_MAX) {
+        return fa::fail(FA_EINVAL, w + "splits * query blocks exceed the grid limit");
+    }
+    return FA_OK;
+}
+
+static int splitkv_run(const fa_params& p, float* lse, const fa::SplitPlan& sp, void* workspace,
+                       void* stream) {
+    const fa::Scale sc = fa::scale_of(p.softmax_scale);
+    auto s = static_cast<hipStream_t>(stream);
+    return fa::with_split_row(p.head_dim, p.causal != 0, [&](auto row) {
+        return fa::splitkv<typename decltype(row)::T>(p, lse, sp, workspace, sc, s);
+    });
+}
+
 int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits,
                          void* workspace, uint64_t workspace_bytes, void* stream) {
     fa::g_last_error.clear();
-    int rc = validate(params, "flash_fwd_splitkv");
+    fa::SplitPlan sp{};
+    const int rc = splitkv_checks(params, lse, num_splits, "flash_fwd_splitkv", &sp);
     if (rc != FA_OK) return rc;
-    const fa_params& p = *params;
-    if (num_splits < 0) return fa::fail(FA_EINVAL, "flash_fwd_splitkv: num_splits must be >= 0");
-    if (lse != nullptr && (reinterpret_cast<uintptr_t>(lse) & 3U) != 0) {
-        return fa::fail(FA_EINVAL, "flash_fwd_splitkv: lse must be 4-byte aligned");
-    }
-    const fa::SplitPlan sp = fa::split_plan(p, num_splits);
-    if (static_cast<int64_t>(p.batch) * p.heads * fa::g::ceil_div(p.seqlen, sp.block_q) *
-            sp.n_splits > INT32_MAX) {
-        return fa::fail(FA_EINVAL, "flash_fwd_splitkv: splits * query blocks exceed the grid limit");
-    }
     if (workspace == nullptr || !fa::aligned16(workspace)) {
         return fa::fail(FA_EINVAL, "flash_fwd_splitkv: workspace must be non-null and 16-byte aligned");
     }
@@ -2102,11 +2163,27 @@ int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits
         return fa::fail(FA_EINVAL, "flash_fwd_splitkv: workspace too small: need " +
                                        std::to_string(sp.workspace_bytes) + " bytes");
     }
-    const fa::Scale sc = fa::scale_of(p.softmax_scale);
-    auto s = static_cast<hipStream_t>(stream);
-    return fa::with_split_row(p.head_dim, p.causal != 0, [&](auto row) {
-        return fa::splitkv<typename decltype(row)::T>(p, lse, sp, workspace, sc, s);
-    });
+    return splitkv_run(*params, lse, sp, workspace, stream);
+}
+
+int fa_flash_fwd_splitkv_static(const fa_params* params, float* lse, int32_t num_splits,
+                                void* stream) {
+    fa::g_last_error.clear();
+    fa::SplitPlan sp{};
+    const int rc = splitkv_checks(params, lse, num_splits, "flash_fwd_splitkv_static", &sp);
+    if (rc != FA_OK) return rc;
+    if (sp.workspace_bytes > FA_STATIC_SCRATCH_BYTES) {
+        return fa::fail(FA_EINVAL, "flash_fwd_splitkv_static: the plan needs " +
+                                       std::to_string(sp.workspace_bytes) +
+                                       " bytes of workspace, more than the static scratch of " +
+                                       std::to_string(FA_STATIC_SCRATCH_BYTES) +
+                                       " bytes; pass a smaller num_splits or call "
+                                       "fa_flash_fwd_splitkv with a workspace");
+    }
+    void* ws = nullptr;
+    const int src = fa::static_scratch(&ws);
+    if (src != FA_OK) return src;
+    return splitkv_run(*params, lse, sp, ws, stream);
 }
 
 }  // extern "C"

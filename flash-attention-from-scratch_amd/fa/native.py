@@ -76,6 +76,9 @@ def lib() -> ctypes.CDLL:
                                         ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint64,
                                         ctypes.c_void_p]
     so.fa_flash_fwd_splitkv.restype = ctypes.c_int
+    so.fa_flash_fwd_splitkv_static.argtypes = [ctypes.POINTER(FaParams), ctypes.c_void_p,
+                                               ctypes.c_int32, ctypes.c_void_p]
+    so.fa_flash_fwd_splitkv_static.restype = ctypes.c_int
     so.fa_last_error.argtypes = []
     so.fa_last_error.restype = ctypes.c_char_p
     so.fa_tile_config.argtypes = [ctypes.POINTER(FaParams), ctypes.POINTER(FaTileInfo)]
@@ -129,6 +132,18 @@ def flash_fwd_splitkv(params: FaParams, lse: int | None, num_splits: int, worksp
     rc = so.fa_flash_fwd_splitkv(ctypes.byref(params), ctypes.c_void_p(lse or 0), num_splits,
                                  ctypes.c_void_p(workspace), workspace_bytes,
                                  ctypes.c_void_p(stream or 0))
+    return rc, so.fa_last_error().decode()
+
+
+STATIC_SCRATCH_BYTES = 64 << 20  # FA_STATIC_SCRATCH_BYTES of include/fa_hip.h
+
+
+def flash_fwd_splitkv_static(params: FaParams, lse: int | None, num_splits: int,
+                             stream: int | None = None) -> tuple[int, str]:
+    """Calls fa_flash_fwd_splitkv_static (the library's own static scratch as workspace)."""
+    so = lib()
+    rc = so.fa_flash_fwd_splitkv_static(ctypes.byref(params), ctypes.c_void_p(lse or 0),
+                                        num_splits, ctypes.c_void_p(stream or 0))
     return rc, so.fa_last_error().decode()
 
 

@@ -108,6 +108,21 @@ int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info
 int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits,
                          void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* fa_flash_fwd_splitkv without a workspace argument and without any allocation: the partial
+ * results go to a static scratch array of FA_STATIC_SCRATCH_BYTES (64 MiB) that the library
+ * holds on every GPU it runs on until the process ends (its device address is looked up once
+ * per device, on the first call with that device current). For callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. No counterpart in the reference. Same arguments, checks and results (bitwise) as
+ * fa_flash_fwd_splitkv with the same num_splits; returns FA_EINVAL, launching nothing, when the
+ * plan's workspace_bytes exceeds the scratch (pass a smaller num_splits then). Every call on a
+ * GPU shares that GPU's scratch: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialized by the caller. The current HIP device must be the device of
+ * `stream`. */
+#define FA_STATIC_SCRATCH_BYTES (64ULL << 20)
+int fa_flash_fwd_splitkv_static(const fa_params* params, float* lse, int32_t num_splits,
+                                void* stream);
+
 /* Tile geometry fa_flash_fwd launches for these parameters: query rows per workgroup, keys per
  * tile, wavefronts per workgroup and LDS bytes per workgroup. The choice depends on variant,
  * head_dim, causal, seqlen and batch * heads (small grids get smaller workgroups); the four
