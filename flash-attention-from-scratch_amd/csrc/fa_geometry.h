@@ -145,7 +145,9 @@ constexpr int st_key(int lane, int nb, int r) { return 32 * nb + mfma32_c_row(la
 constexpr int pv_key(int lane, int i) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
 // ---- Work decomposition ---------------------------------------------------------------------
-constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+// ceil(a / b) for a >= 0, b > 0, without forming a + b - 1 (which overflows for a near
+// INT32_MAX).
+constexpr int ceil_div(int a, int b) { return a / b + (a % b > 0 ? 1 : 0); }
 
 // Number of K/V tiles a workgroup whose first query row is q0 visits. Causal workgroups stop
 // at the tile holding their last query's diagonal (tiles above it are fully masked);

@@ -2115,6 +2115,9 @@ int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info
         return fa::fail(FA_EINVAL, "fa_splitkv_plan: head_dim must be 64 or 128, got " +
                                        std::to_string(p.head_dim));
     }
+    if (static_cast<int64_t>(p.seqlen) * p.head_dim > INT32_MAX) {
+        return fa::fail(FA_EINVAL, "fa_splitkv_plan: seqlen * head_dim must be below 2^31");
+    }
     if (num_splits < 0) return fa::fail(FA_EINVAL, "fa_splitkv_plan: num_splits must be >= 0");
     const fa::SplitPlan sp = fa::split_plan(p, num_splits);
     *out = fa_splitkv_info{sp.n_splits, sp.tiles_per_split, sp.block_q, sp.block_k,
