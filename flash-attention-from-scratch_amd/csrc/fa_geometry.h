@@ -204,9 +204,9 @@ constexpr KeyRange split_range(int n_all, int tps, int split) {
 }
 
 // Workgroup id -> (batch*head index, query block). Consecutive ids share the query block and
-// walk the heads; the hardware deals consecutive ids round-robin to the 8 XCDs, so each XCD
-// keeps a fixed subset of heads (whose K/V then stay in that XCD's L2) when B*H is a multiple
-// of 8. Causal runs the longest query blocks first (as csrc/kernels/flash_fwd.cu:183-185).
+// walk the heads; causal runs the longest query blocks first (as
+// csrc/kernels/flash_fwd.cu:183-185). Used by the split-KV partial passes (within one key
+// range) and by work_of_xcd for causal grids.
 struct Work {
     int bh;
     int qb;
@@ -214,6 +214,29 @@ struct Work {
 constexpr Work work_of(int block_id, int bh_count, int n_qblocks, bool causal) {
     const int qi = block_id / bh_count;
     return Work{block_id % bh_count, causal ? n_qblocks - 1 - qi : qi};
+}
+
+// Workgroup id -> (batch*head index, query block), XCD-aware for non-causal grids. MI355X
+// deals workgroup ids round-robin to its kXcds XCDs (id % 8), and each XCD has its own L2. The
+// non-causal (head, query block) items are laid out head-major and XCD x receives one
+// contiguous eighth of them (slot s = id / 8 is the s-th item of that eighth), so the query
+// blocks of a head run on one XCD at about the same time and share its K/V in that XCD's L2,
+// whatever B*H is; all items are equal, so the XCDs stay balanced. (work_of walks the heads with
+// consecutive ids, which scatters a head's query blocks in time: on many short heads, e.g.
+// 512 heads of 2048 keys, their K/V are then re-read from HBM by every query block.)
+// Causal grids keep work_of's global longest-first order: measured on MI355X, its tail (the
+// shortest query blocks last, everywhere at once) is worth more than the L2 locality, which
+// head-grouped orders buy only by mixing long and short blocks late in the launch.
+constexpr int kXcds = 8;
+constexpr Work work_of_xcd(int block_id, int bh_count, int n_qblocks, bool causal) {
+    if (causal) return work_of(block_id, bh_count, n_qblocks, causal);
+    const int x = block_id % kXcds;
+    const int slot = block_id / kXcds;
+    const long long total = static_cast<long long>(bh_count) * n_qblocks;
+    const long long per = total / kXcds;
+    const long long extra = total % kXcds;
+    const long long t = x * per + (x < extra ? x : extra) + slot;
+    return Work{static_cast<int>(t / n_qblocks), static_cast<int>(t % n_qblocks)};
 }
 
 }  // namespace fa::geom

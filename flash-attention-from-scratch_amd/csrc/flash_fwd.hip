@@ -248,6 +248,60 @@ __device__ __forceinline__ void rescale_o(f32x16 (&oacc)[T::DB], float alpha) {
     for (int db = 0; db < T::DB; ++db) oacc[db] *= alpha;
 }
 
+// Optimistic softmax of one tile (LAZY tiles): p = exp2(s*c - m) against the running max m,
+// without the tile's row max. If some p of the wave reaches 65520 (a score above m by 16 log2
+// units or more; also the first tile, where m = -inf, and a row whose keys are all masked so
+// far, where -inf - -inf is NaN), the fp16 pack gives inf or NaN and so does the lane's row sum:
+// `overflow` is set (wave-uniform), l is left alone and the caller redoes the tile with
+// softmax_tile. Otherwise every p lies in [0, 65504], held by fp16 at its usual precision and by
+// the fp32 accumulators of O and l, so the result is the same softmax against a different valid
+// reference point. Each group of 8 exponentials is packed at once, which keeps 8 temporaries
+// live instead of 16 * NB (the simple d=64 tiles must stay within 128 VGPRs for four waves per
+// SIMD, whose interleaving hides the exponentials' latency).
+template <class T>
+__device__ __forceinline__ void softmax_optimistic(const f32x16 (&s)[T::NB], float scale_log2,
+                                                   float m_run, float& l_run, bool& overflow,
+                                                   f16x8 (&p)[T::NB][2]) {
+    float sum0 = 0.0F;
+    float sum1 = 0.0F;
+#pragma unroll
+    for (int nb = 0; nb < T::NB; ++nb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float e[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) e[r] = exp2_fast(fmaf(s[nb][8 * h + r], scale_log2, -m_run));
+            p[nb][h] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+            if (h == 0) {
+                sum0 = sum8_f16(p[nb][h], sum0);
+            } else {
+                sum1 = sum8_f16(p[nb][h], sum1);
+            }
+        }
+    const float sum = sum0 + sum1;
+    overflow = wave_any(!(sum < INFINITY));
+    l_run = overflow ? l_run : l_run + sum;
+}
+
+// Softmax of one tile for the simple and key-split schedules: optimistic first when the tile
+// is LAZY (FA_OPTIMISTIC), exact (softmax_tile, with the rescale of O) when that overflows or
+// the tile is not LAZY.
+template <class T>
+__device__ __forceinline__ void softmax_any(const f32x16 (&s)[T::NB], float scale_log2,
+                                            float& m_run, float& l_run, f32x16 (&oacc)[T::DB],
+                                            f16x8 (&p)[T::NB][2]) {
+    bool exact = true;
+    if constexpr (T::LAZY && FA_OPTIMISTIC) {
+        softmax_optimistic<T>(s, scale_log2, m_run, l_run, exact, p);
+    }
+    if (exact) {
+        float alpha;
+        bool rescale;
+        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (rescale) rescale_o<T>(oacc, alpha);
+    }
+}
+
 // O^T += V^T P^T for one tile: NB x 2 x DB MFMAs, V^T fragments by transposed LDS reads.
 template <class T>
 __device__ __forceinline__ void pv_tile(const char* vl, const Frag<T>& fr,
@@ -394,8 +448,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int items = bh_count * n_qblocks;
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
-    const g::Work w = g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
-                                 n_qblocks, CAUSAL);
+    const g::Work w = SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                                         n_qblocks, CAUSAL)
+                            : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const f16* kh = k + head;
     const f16* vh = v + head;
@@ -441,10 +496,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         qk_tile<T>(kbuf(j & 1), fr, qf, s);
         if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
-        float alpha;
-        bool rescale;
-        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale_o<T>(oacc, alpha);
+        softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
         pv_tile<T>(vbuf(j & 1), fr, p, oacc);
     }
     if constexpr (SPLIT) {
@@ -520,7 +572,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int half = wave / T::NW;  // 0: even key tiles, 1: odd key tiles
     const int wq = wave % T::NW;    // which 32 query rows
-    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const g::Work w = g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const f16* kh = k + head;
     const f16* vh = v + head;
@@ -562,10 +614,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
         qk_tile<T>(kbuf(j & 1), fr, qf, s);
         if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
-        float alpha;
-        bool rescale;
-        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale_o<T>(oacc, alpha);
+        softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
         pv_tile<T>(vbuf(j & 1), fr, p, oacc);
     }
 
@@ -823,7 +872,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
-    const g::Work w = g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const g::Work w = g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const f16* kh = k + head;
     const f16* vh = v + head;
@@ -944,8 +993,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
 // or 4 phases before its first read, and replaces a tile whose last read was in an earlier
 // phase. Diagonal and tail tiles are masked inside the steady phases; only the last tile, which
 // has no successor to prefetch, goes through general_tiles16 afterwards.
+// Wave priorities (s_setprio) of the ping-pong's matrix phase and softmax phase.
 #ifndef FA_PP_PRIO
 #define FA_PP_PRIO 1
+#endif
+#ifndef FA_PP_SPRIO
+#define FA_PP_SPRIO 0
 #endif
 // Scheduler pattern: N times {R DS reads, V VALU instructions} (sched_group_barrier masks
 // 0x100 DS read, 0x002 VALU | 0x400 transcendental).
@@ -1427,7 +1480,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
     const g::Work w = SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
                                          n_qblocks, CAUSAL)
-                            : g::work_of(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+                            : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const int q0 = w.qb * T::BR;
     const int qw = q0 + wave * 32;  // first query of this wave (Q loads, O stores)
@@ -1552,7 +1605,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                     refill(jj + 4, Rj1{}, jj + 3, Rj{});
                 }
             });
-            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_s_setprio(FA_PP_SPRIO);
             end_phase<G == 0>();
         };
         int jj = 0;

@@ -4,6 +4,8 @@
 #
 #   dev/counters.sh [name] [B H N D causal [variant]]     default: cfg4 1 16 16384 128 0 opt
 #   OUT=gpurun_out/counters/x dev/counters.sh cfg2c 4 16 4096 128 1
+#   FA_DEV_ARGS="--std 0.5 --boost-keys 0.01:8" dev/counters.sh cfg5 16 32 2048 64 1
+#       (FA_DEV_ARGS: extra fa_dev input options, e.g. the many-heads config's inputs)
 #
 # Writes OUT (default gpurun_out/counters/<name>): one rocprofv3 directory per pass and
 # summary.md, made by dev/counters.py. Passes (rocprofv3 collects each counter set in one run
@@ -33,7 +35,8 @@ OUT=${OUT:-gpurun_out/counters/$NAME}
 mkdir -p "$OUT"
 export TMPDIR=${TMPDIR:-/tmp}
 # 1 checked launch, warmup launches for WARMUP_MS (default 100 ms: the clock ramps), 3 timed
-RUN=("$BIN" "${ARGS[@]}" 3 "$VARIANT" --warmup-ms "${WARMUP_MS:-100}")
+read -r -a EXTRA <<< "${FA_DEV_ARGS:-}"
+RUN=("$BIN" "${ARGS[@]}" 3 "$VARIANT" --warmup-ms "${WARMUP_MS:-100}" "${EXTRA[@]}")
 
 pass() {
     local name=$1
@@ -57,6 +60,6 @@ pass fetch --pmc FETCH_SIZE
 pass write --pmc WRITE_SIZE
 
 python3 "$here/counters.py" "$OUT" --shape "${ARGS[@]}" --variant "$VARIANT" \
-    --command "dev/counters.sh $NAME ${ARGS[*]} $VARIANT" > "$OUT/summary.md"
+    --command "${FA_DEV_ARGS:+FA_DEV_ARGS=\"$FA_DEV_ARGS\" }dev/counters.sh $NAME ${ARGS[*]} $VARIANT" > "$OUT/summary.md"
 echo "summary: $OUT/summary.md" >&2
 cat "$OUT/summary.md"

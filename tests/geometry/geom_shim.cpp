@@ -48,6 +48,11 @@ void geom_split_range(int n_all, int tps, int split, int* begin, int* count) {
     *begin = r.begin;
     *count = r.count;
 }
+void geom_work_of_xcd(int block_id, int bh_count, int n_qblocks, int causal, int* bh, int* qb) {
+    const g::Work w = g::work_of_xcd(block_id, bh_count, n_qblocks, causal != 0);
+    *bh = w.bh;
+    *qb = w.qb;
+}
 void geom_work_of(int block_id, int bh_count, int n_qblocks, int causal, int* bh, int* qb) {
     const g::Work w = g::work_of(block_id, bh_count, n_qblocks, causal != 0);
     *bh = w.bh;

@@ -26,6 +26,7 @@ LIB = Path(__file__).resolve().parent / "geometry" / "libfa_geom.so"
 def geo():
     so = ctypes.CDLL(str(LIB))
     so.geom_work_of.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
+    so.geom_work_of_xcd.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_split_range.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 2
     return so
 
@@ -365,6 +366,57 @@ def test_work_map_is_a_bijection(geo, causal):
                 assert qb.value <= prev  # longest (highest) query blocks launch first
             prev = qb.value
         assert len(seen) == bhc * nqb
+
+
+def _xcd_map(geo, bhc, nqb, causal):
+    bh, qb = ctypes.c_int(), ctypes.c_int()
+    out = []
+    for bid in range(bhc * nqb):
+        geo.geom_work_of_xcd(bid, bhc, nqb, causal, ctypes.byref(bh), ctypes.byref(qb))
+        out.append((bh.value, qb.value))
+    return out
+
+
+XCD_SHAPES = [(1, 1), (1, 7), (3, 5), (8, 8), (12, 64), (16, 64), (16, 128), (64, 16),
+              (512, 8), (24, 3), (40, 17), (7, 9)]
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_xcd_work_map_is_a_bijection(geo, causal):
+    for bhc, nqb in XCD_SHAPES:
+        items = _xcd_map(geo, bhc, nqb, causal)
+        assert all(0 <= h < bhc and 0 <= q < nqb for h, q in items)
+        assert len(set(items)) == bhc * nqb, (bhc, nqb)
+
+
+def test_xcd_work_map_keeps_heads_together(geo):
+    """Workgroup id b runs on XCD b % 8. Non-causal: each XCD holds one contiguous run of the
+    head-major items, so a head spans one XCD when B*H is a multiple of 8 and otherwise only as
+    many as its query blocks need (two when it has fewer than an eighth of the items), and the
+    XCDs get item counts within one of each other. Causal: work_of's global longest-first
+    order."""
+    for bhc, nqb in XCD_SHAPES:
+        for causal in (0, 1):
+            items = _xcd_map(geo, bhc, nqb, causal)
+            if causal:
+                bh, qb = ctypes.c_int(), ctypes.c_int()
+                for bid, item in enumerate(items):
+                    geo.geom_work_of(bid, bhc, nqb, causal, ctypes.byref(bh), ctypes.byref(qb))
+                    assert item == (bh.value, qb.value)
+                continue
+            xcds_of_head = {}
+            per_xcd = [[] for _ in range(8)]
+            for bid, (h, q) in enumerate(items):
+                xcds_of_head.setdefault(h, set()).add(bid % 8)
+                per_xcd[bid % 8].append((h, q))
+            counts = [len(x) for x in per_xcd]
+            assert max(counts) - min(counts) <= 1
+            per = max(1, bhc * nqb // 8)
+            span = 1 if bhc % 8 == 0 else -(-nqb // per) + 1
+            assert max(len(v) for v in xcds_of_head.values()) <= span
+            for lst in per_xcd:  # contiguous head-major runs, in order
+                flat = [h * nqb + q for h, q in lst]
+                assert flat == list(range(flat[0], flat[0] + len(flat))) if flat else True
 
 
 def test_split_ranges_partition_each_query_block(geo):
