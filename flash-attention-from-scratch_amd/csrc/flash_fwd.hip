@@ -442,7 +442,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
     float* __restrict__ lse_part) {
-    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+    // One LDS object per buffer, and the buffer of each tile fixed at compile time (the loop is
+    // unrolled by two): the compiler then sees that the refill of one buffer cannot alias the
+    // reads of the other and waits for a tile's DMA only at the barrier that starts the tile.
+    // With one array it would wait for the next tile's refill before this tile's P.V reads.
+    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -466,13 +473,20 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     // plain one the extra exit costs the causal d=64 tile 30 VGPRs (and half its occupancy).
     if (SPLIT && range.count == 0) return;
 
-    // LDS: [K0 | K1 | V0 | V1]; buffer b of K at b*TILE_BYTES, of V at (2+b)*TILE_BYTES.
-    auto kbuf = [&](int b) { return smem + b * T::TILE_BYTES; };
-    auto vbuf = [&](int b) { return smem + (2 + b) * T::TILE_BYTES; };
+    // Tile t lives in buffer t % 2.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    auto kbuf = [&](auto b) { return decltype(b)::value == 0 ? k_lds0 : k_lds1; };
+    auto vbuf = [&](auto b) { return decltype(b)::value == 0 ? v_lds0 : v_lds1; };
 
     const TileDma<T> dma(wave, lane);
-    load_tile<T>(kh, j_begin * T::BC, n, kbuf(j_begin & 1), dma);
-    load_tile<T>(vh, j_begin * T::BC, n, vbuf(j_begin & 1), dma);
+    if (j_begin & 1) {
+        load_tile<T>(kh, j_begin * T::BC, n, kbuf(I1{}), dma);
+        load_tile<T>(vh, j_begin * T::BC, n, vbuf(I1{}), dma);
+    } else {
+        load_tile<T>(kh, j_begin * T::BC, n, kbuf(I0{}), dma);
+        load_tile<T>(vh, j_begin * T::BC, n, vbuf(I0{}), dma);
+    }
     f16x8 qf[T::KK];
     load_q<T>(q + head, qrow, n, lane, negate_q, qf);
     const Frag<T> fr(lane);
@@ -483,22 +497,36 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     float m_run = -INFINITY;  // running max of this lane's query, log2 domain (scaled)
     float l_run = 0.0F;       // this lane's partial row sum (its 16 keys of each 32-key block)
 
-    for (int j = j_begin; j < n_tiles; ++j) {
+    // Tile j in buffer B = j % 2: barrier, refill of the other buffer with tile j+1, then
+    // S = QK^T, mask, softmax and O += PV.
+    auto tile = [&](int j, auto b) {
+        constexpr int B = decltype(b)::value;
+        using Other = std::integral_constant<int, 1 - B>;
         wait_vmem();
         __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
         if (j + 1 < n_tiles) {
-            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf((j + 1) & 1), dma);
-            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf((j + 1) & 1), dma);
+            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf(Other{}), dma);
+            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf(Other{}), dma);
         }
         const int kt = j * T::BC;
-        if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) continue;  // wave-uniform
+        if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) return;  // wave-uniform
         f32x16 s[T::NB];
-        qk_tile<T>(kbuf(j & 1), fr, qf, s);
+        qk_tile<T>(kbuf(b), fr, qf, s);
         if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
         softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
-        pv_tile<T>(vbuf(j & 1), fr, p, oacc);
+        pv_tile<T>(vbuf(b), fr, p, oacc);
+    };
+    int j = j_begin;
+    if (j & 1) {
+        tile(j, I1{});
+        ++j;
     }
+    for (; j + 2 <= n_tiles; j += 2) {
+        tile(j, I0{});
+        tile(j + 1, I1{});
+    }
+    if (j < n_tiles) tile(j, I0{});
     if constexpr (SPLIT) {
         const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
         store_partial<T>(o_part + part * n * T::D, lse_part + part * n, qrow, n, lane, m_run,
@@ -1576,9 +1604,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             using Rj = std::integral_constant<int, R>;
             using Rj1 = std::integral_constant<int, (R + 1) % 3>;
             using Rj2 = std::integral_constant<int, (R + 2) % 3>;
-            // softmax phase S_jj
-            if (g::tile_needs_mask(nk, jj * T::BC, T::BC, qk, CAUSAL)) {
-                mask16<T, CAUSAL>(s, jj * T::BC, nk, qk, lane);
+            // softmax phase S_jj. Only causal steady tiles can need a mask: without causality
+            // the one tile that can reach past the sequence end is the last, which runs in
+            // general_tiles16. (Left to the compiler, the non-causal test is turned into 32
+            // unconditional compare/select VALU instructions per tile.)
+            if constexpr (CAUSAL) {
+                if (g::tile_needs_mask(nk, jj * T::BC, T::BC, qk, CAUSAL)) {
+                    mask16<T, CAUSAL>(s, jj * T::BC, nk, qk, lane);
+                }
             }
             f16x8 kf[G::KB][G::DC];
             f16x8 vf[G::KS][G::DB];

@@ -20,6 +20,8 @@ RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" /
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
 SIMPLE, PIPE, KSPLIT, PINGPONG16 = 0, 1, 3, 4
+# flash_fwd_kernel<Tile, CAUSAL, SPLIT>: the split-KV build ends its template arguments in Lb1E
+SPLIT_SUFFIX_RE = re.compile(r"ELb[01]ELb1EEEv")
 
 
 def _load():
@@ -39,6 +41,10 @@ def _min_occupancy(name: str) -> int:
     if "flash_fwd_pipelined" in name:
         return 3 if d == 64 else 1
     assert "flash_fwd_kernel" in name and sched == SIMPLE
+    if SPLIT_SUFFIX_RE.search(name) and d == 64:
+        # the split-KV partial pass of causal d=64 (4-wave tile): its extra range bookkeeping
+        # takes it to 148 VGPRs, three waves per SIMD, measured as fast as the four-wave build
+        return 3
     return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
 
 
