@@ -593,8 +593,20 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
     float* /*lse_part*/) {
     static_assert(T::KS == 2, "two key halves");
-    // Tiles: half h, buffer b: K at (2h + b) * 2 tiles, V right after. Reused by the merge.
-    __shared__ __attribute__((aligned(1024))) char smem[T::LDS_BYTES];
+    // One LDS object per (key half, buffer) for K and V, and the buffer of each step fixed at
+    // compile time (the step loop is unrolled by two): the compiler then sees that a refill
+    // cannot alias the reads of the other buffer and waits for DMA only at the step barrier.
+    // Two of the objects are reused by the merge at the end.
+    __shared__ __attribute__((aligned(1024))) char k00[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k01[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k10[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k11[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v00[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v01[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v10[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v11[T::TILE_BYTES];
+    static_assert(T::NW * 128 * 4 <= T::TILE_BYTES && T::NW * 64 * 16 * 4 <= T::TILE_BYTES,
+                  "the merge's (m, l) and O blocks fit in one tile buffer each");
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -609,13 +621,27 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const int qrow = qw + (lane & 31);
     const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
     const int n_steps = (n_tiles + 1) / 2;
-    auto kbuf = [&](int b) { return smem + (2 * half + b) * 2 * T::TILE_BYTES; };
-    auto vbuf = [&](int b) { return kbuf(b) + T::TILE_BYTES; };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    // Buffer b of key half H (both compile-time).
+    auto kbuf = [&](auto hc, auto b) {
+        constexpr int H = decltype(hc)::value;
+        return decltype(b)::value == 0 ? (H ? k10 : k00) : (H ? k11 : k01);
+    };
+    auto vbuf = [&](auto hc, auto b) {
+        constexpr int H = decltype(hc)::value;
+        return decltype(b)::value == 0 ? (H ? v10 : v00) : (H ? v11 : v01);
+    };
 
     const TileDma<T> dma(wq, lane);
     if (half < n_tiles) {
-        load_tile<T>(kh, half * T::BC, n, kbuf(0), dma);
-        load_tile<T>(vh, half * T::BC, n, vbuf(0), dma);
+        if (half) {
+            load_tile<T>(kh, T::BC, n, kbuf(I1{}, I0{}), dma);
+            load_tile<T>(vh, T::BC, n, vbuf(I1{}, I0{}), dma);
+        } else {
+            load_tile<T>(kh, 0, n, kbuf(I0{}, I0{}), dma);
+            load_tile<T>(vh, 0, n, vbuf(I0{}, I0{}), dma);
+        }
     }
     f16x8 qf[T::KK];
     load_q<T>(q + head, qrow, n, lane, negate_q, qf);
@@ -627,29 +653,45 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     float m_run = -INFINITY;
     float l_run = 0.0F;
 
-    for (int j = 0; j < n_steps; ++j) {
+    // Step j in buffer B = j % 2: key half H's tile 2j + H.
+    auto step = [&](int j, auto hc, auto b) {
+        constexpr int H = decltype(hc)::value;
+        using Other = std::integral_constant<int, 1 - decltype(b)::value>;
         wait_vmem();
         __syncthreads();  // step j's tiles are in LDS; step j-1's buffers are free
-        const int tn = 2 * (j + 1) + half;
+        const int tn = 2 * (j + 1) + H;
         if (tn < n_tiles) {
-            load_tile<T>(kh, tn * T::BC, n, kbuf((j + 1) & 1), dma);
-            load_tile<T>(vh, tn * T::BC, n, vbuf((j + 1) & 1), dma);
+            load_tile<T>(kh, tn * T::BC, n, kbuf(hc, Other{}), dma);
+            load_tile<T>(vh, tn * T::BC, n, vbuf(hc, Other{}), dma);
         }
-        const int t = 2 * j + half;
+        const int t = 2 * j + H;
         const int kt = t * T::BC;
-        if (t >= n_tiles || qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) continue;
+        if (t >= n_tiles || qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) return;
         f32x16 s[T::NB];
-        qk_tile<T>(kbuf(j & 1), fr, qf, s);
+        qk_tile<T>(kbuf(hc, b), fr, qf, s);
         if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
         softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
-        pv_tile<T>(vbuf(j & 1), fr, p, oacc);
+        pv_tile<T>(vbuf(hc, b), fr, p, oacc);
+    };
+    auto steps = [&](auto hc) {
+        int j = 0;
+        for (; j + 2 <= n_steps; j += 2) {
+            step(j, hc, I0{});
+            step(j + 1, hc, I1{});
+        }
+        if (j < n_steps) step(j, hc, I0{});
+    };
+    if (half) {  // wave-uniform; both halves pass the same number of barriers
+        steps(I1{});
+    } else {
+        steps(I0{});
     }
 
     // Merge through LDS: (m, l) of the odd half, then O one 32-column block at a time.
     const float l_tot = sum_xor32(l_run);
-    float* ml = reinterpret_cast<float*>(smem);       // [NW][64][2]
-    float* ob = ml + T::NW * 128;                     // [NW][64][16]
+    float* ml = reinterpret_cast<float*>(k00);        // [NW][64][2]
+    float* ob = reinterpret_cast<float*>(v00);        // [NW][64][16]
     const int slot = wq * 64 + lane;
     wait_vmem();
     __syncthreads();  // every wave is done with the tile buffers
