@@ -64,12 +64,12 @@ namespace g = fa::geom;
 #define FA_OPTIMISTIC 1
 #endif
 
-// Main-loop schedules: SIMPLE (flash_fwd_kernel), PIPE (flash_fwd_pipelined: QK of tile j+1
-// interleaved with the softmax of tile j in each wave), KSPLIT (flash_fwd_ksplit: two waves per
-// 32 query rows on alternate key tiles), PINGPONG16 (flash_fwd_pingpong16: two groups of waves
-// alternate between an MFMA-only phase and a softmax phase, on 16x16x32 MFMAs; the table's
-// long-sequence rows). The values are those the -D tile overrides name.
-enum Sched { SIMPLE = 0, PIPE = 1, KSPLIT = 3, PINGPONG16 = 4 };
+// Main-loop schedules: SIMPLE (flash_fwd_kernel: each wave runs QK, softmax and PV of a tile in
+// turn), KSPLIT (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles),
+// PINGPONG16 (flash_fwd_pingpong16: two groups of waves alternate between an MFMA-only phase and
+// a softmax phase, on 16x16x32 MFMAs; the table's long d = 128 rows). The values are those the
+// -D tile overrides name.
+enum Sched { SIMPLE = 0, KSPLIT = 3, PINGPONG16 = 4 };
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
@@ -318,47 +318,6 @@ __device__ __forceinline__ void pv_tile(const char* vl, const Frag<T>& fr,
                 const f16x8 a = {lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
                 oacc[db] = mfma32(a, p[nb][h], oacc[db]);
             }
-}
-
-// K fragments of a whole tile into registers (NB*KK operands of 4 VGPRs).
-template <class T>
-__device__ __forceinline__ void load_k_frags(const char* kl, const Frag<T>& fr,
-                                             f16x8 (&kf)[T::NB][T::KK]) {
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < T::KK; ++kk)
-            kf[nb][kk] =
-                *reinterpret_cast<const f16x8*>(kl + fr.koff[kk] + nb * 32 * T::ROW_BYTES);
-}
-
-// V^T fragments of a whole tile into registers (NB*2*DB operands of 4 VGPRs), so their LDS
-// latency can be covered by other work before pv_frags consumes them.
-template <class T>
-__device__ __forceinline__ void load_v_frags(const char* vl, const Frag<T>& fr,
-                                             f16x8 (&vf)[T::NB][2][T::DB]) {
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int db = 0; db < T::DB; ++db) {
-                const char* base = vl + (32 * nb + 16 * h) * T::ROW_BYTES;
-                const f16x4 lo = lds_read_tr16(base + fr.voff[db][0]);
-                const f16x4 up = lds_read_tr16(base + fr.voff[db][1]);
-                vf[nb][h][db] = f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
-            }
-}
-
-template <class T>
-__device__ __forceinline__ void pv_frags(const f16x8 (&vf)[T::NB][2][T::DB],
-                                         const f16x8 (&p)[T::NB][2], f32x16 (&oacc)[T::DB]) {
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int db = 0; db < T::DB; ++db) oacc[db] = mfma32(vf[nb][h][db], p[nb][h], oacc[db]);
 }
 
 // Base-2 log-sum-exp of the row's scaled scores, m + log2(l): the lane's running max m (the
@@ -734,314 +693,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
         store_o_tot<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n,
                        lane, m_new, l_new, oacc);
     }
-}
-
-// Scheduler pattern: N times {one MFMA, then up to VALU_PER VALU instructions}. Masks of
-// __builtin_amdgcn_sched_group_barrier (LLVM AMDGPU): 0x008 MFMA, 0x002 VALU.
-#ifndef FA_VALU_PER_MFMA
-#define FA_VALU_PER_MFMA 8
-#endif
-template <int VALU_PER, int... I>
-__device__ __forceinline__ void sched_mfma_valu(std::integer_sequence<int, I...>) {
-    ((__builtin_amdgcn_sched_group_barrier(0x008, 1, 0),
-      __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER + 0 * I, 0)),
-     ...);
-}
-
-// Region pattern of the steady-state iteration: the DMA refill (0x020 VMEM read) and the K
-// fragment reads (0x100 DS read) first, two {MFMA, VALU} stages, then the V^T fragment reads,
-// then the remaining stages. The K reads come before the V reads so the first MFMA waits for
-// its own operand only.
-template <int VALU_PER, int NK, int NV, int NDMA, int M>
-__device__ __forceinline__ void sched_steady_region() {
-    __builtin_amdgcn_sched_group_barrier(0x020, NDMA, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, NK, 0);
-    sched_mfma_valu<VALU_PER>(std::make_integer_sequence<int, 2>{});
-    __builtin_amdgcn_sched_group_barrier(0x100, NV, 0);
-    sched_mfma_valu<VALU_PER>(std::make_integer_sequence<int, M - 2>{});
-}
-
-// ---- QK of tile j+1 interleaved with the softmax of tile j -------------------------------------
-// NB*KK stages; stage m issues MFMA m of S^T_{j+1} = K_{j+1} Q^T and then one slice of tile j's
-// softmax: the first quarter of the stages reduce the row max over the lane's 16*NB scores, the
-// next one combines the halves of the wave and fixes the new max, and the rest compute the
-// exponentials; the fp16 packing and row sums follow the last stage. The caller's sched_group_barrier pattern makes the
-// scheduler emit each MFMA followed by about FA_VALU_PER_MFMA VALU instructions, so the VALU
-// work issues while the MFMAs run. Same arithmetic as mask-free softmax_tile.
-template <class T>
-__device__ __forceinline__ void qk_softmax_interleaved(
-    const f16x8 (&kf)[T::NB][T::KK], const f16x8 (&qf)[T::KK], const f32x16 (&s)[T::NB],
-    float scale_log2, float& m_run, float& l_run, float& alpha, bool& rescale,
-    f32x16 (&s_next)[T::NB], f16x8 (&p)[T::NB][2]) {
-    constexpr int M = T::NB * T::KK;   // MFMA stages
-    constexpr int E = 16 * T::NB;      // scores per lane
-    constexpr int M1 = M / 4 > 0 ? M / 4 : 1;
-    constexpr int PER_MAX = (E + M1 - 1) / M1;
-    constexpr int M2 = M - M1 - 1;
-    constexpr int PER_EXP = (E + M2 - 1) / M2;
-    static_assert(M2 >= 1, "need at least one exponential stage");
-    float mx = -INFINITY;
-    float m_use = 0.0F;
-    float sum = 0.0F;
-    float pe[E];
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) s_next[nb] = f32x16{};
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        s_next[m / T::KK] = mfma32(kf[m / T::KK][m % T::KK], qf[m % T::KK], s_next[m / T::KK]);
-        if (m < M1) {
-#pragma unroll
-            for (int e = m * PER_MAX; e < (m + 1) * PER_MAX && e < E; ++e)
-                mx = fmaxf(mx, s[e / 16][e % 16]);
-        } else if (m == M1) {
-            mx = max_xor32(mx) * scale_log2;
-            rescale = wave_any(T::LAZY ? (mx > m_run + 8.0F) : (mx > m_run));
-            const float m_new = rescale ? fmaxf(m_run, mx) : m_run;
-            m_use = (m_new == -INFINITY) ? 0.0F : m_new;
-            alpha = exp2_fast(m_run - m_use);
-            m_run = m_new;
-        } else {
-            const int st = m - M1 - 1;
-#pragma unroll
-            for (int e = st * PER_EXP; e < (st + 1) * PER_EXP && e < E; ++e)
-                pe[e] = exp2_fast(fmaf(s[e / 16][e % 16], scale_log2, -m_use));
-        }
-    }
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) {
-        const float* e = pe + 16 * nb;
-        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
-        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
-        sum = sum8_f16(p[nb][1], sum8_f16(p[nb][0], sum));
-    }
-    l_run = (rescale ? l_run * alpha : l_run) + sum;
-    // Empty asm that reads P and l: keeps their computation in this block. Without it LLVM
-    // sinks the exponentials past the caller's (rarely taken) rescale branch, behind the MFMAs.
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) asm volatile("" ::"v"(p[nb][0]), "v"(p[nb][1]));
-    asm volatile("" ::"v"(l_run));
-}
-
-// ---- QK of tile j+1 interleaved with an optimistic softmax of tile j --------------------------
-// The common case of the steady state needs no row max: with the running max m kept from the
-// last rescale, p = exp2(s*c - m) is computed directly and packed to fp16. If some p of the
-// wave reaches 65520 (its score exceeds m by 16 log2 units or more, including the first tile,
-// where m = -inf) the fp16 pack gives inf and so does the lane's fp32 row sum; then
-// `overflow` is set (wave-uniform) and the caller redoes the tile with the exact softmax,
-// which updates m and rescales O. Otherwise every p lies in [0, 65504], which fp16 holds
-// with its usual 11-bit precision and the fp32 accumulators of O and l hold easily, so the
-// result is the same softmax with a different (valid) reference point m. Stage m issues MFMA m
-// of S^T_{j+1} and a slice of the exponentials; the caller's sched_group_barrier pattern
-// interleaves them.
-template <class T>
-__device__ __forceinline__ void qk_softmax_optimistic(
-    const f16x8 (&kf)[T::NB][T::KK], const f16x8 (&qf)[T::KK], const f32x16 (&s)[T::NB],
-    float scale_log2, float m_run, float& l_run, bool& overflow, f32x16 (&s_next)[T::NB],
-    f16x8 (&p)[T::NB][2]) {
-    constexpr int M = T::NB * T::KK;  // MFMA stages
-    constexpr int E = 16 * T::NB;     // scores per lane
-    constexpr int PER_EXP = (E + M - 1) / M;
-    float pe[E];
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) s_next[nb] = f32x16{};
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        s_next[m / T::KK] = mfma32(kf[m / T::KK][m % T::KK], qf[m % T::KK], s_next[m / T::KK]);
-#pragma unroll
-        for (int e = m * PER_EXP; e < (m + 1) * PER_EXP && e < E; ++e)
-            pe[e] = exp2_fast(fmaf(s[e / 16][e % 16], scale_log2, -m_run));
-    }
-    float sum = 0.0F;
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) {
-        const float* e = pe + 16 * nb;
-        p[nb][0] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
-        p[nb][1] = pack8(e[8], e[9], e[10], e[11], e[12], e[13], e[14], e[15]);
-        sum = sum8_f16(p[nb][1], sum8_f16(p[nb][0], sum));
-    }
-    overflow = wave_any(!(sum < INFINITY));
-    if (!overflow) l_run += sum;
-    // Empty asm that reads P and l: keeps their computation in this block (see
-    // qk_softmax_interleaved).
-#pragma unroll
-    for (int nb = 0; nb < T::NB; ++nb) asm volatile("" ::"v"(p[nb][0]), "v"(p[nb][1]));
-    asm volatile("" ::"v"(l_run));
-}
-
-// ---- tiles outside the steady state ----------------------------------------------------------
-// Tiles j0 .. n_tiles-1 of a wave, one workgroup barrier each: diagonal and tail tiles (masked),
-// the last tile, and tiles a causal wave only waits through. K_t and V_t live in buffer t % NBUF.
-// On entry S_j0 is in s and K_{j0+1} and V_{j0} are resident once the outstanding DMA has landed
-// (any DMA still in flight targets other buffers, or carries the same tile). Per tile: wait,
-// barrier, fragment reads of K_{j+1} and V_j, refill of K_{j+2} and V_{j+1} into buffers no wave
-// reads in this iteration, S_{j+1}, mask, exact softmax, P.V.
-template <class T, bool CAUSAL, int NBUF>
-__device__ __forceinline__ void general_tiles(
-    int j, int n_tiles, int n_act, int n, int qw, int qrow, int lane, const f16* kh, const f16* vh,
-    char* const (&kb)[NBUF], char* const (&vb)[NBUF], const TileDma<T>& dma, const Frag<T>& fr,
-    const f16x8 (&qf)[T::KK], f32x16 (&s)[T::NB], f32x16 (&oacc)[T::DB], float scale_log2,
-    float& m_run, float& l_run) {
-    for (; j < n_tiles; ++j) {
-        wait_vmem();
-        __syncthreads();
-        const bool act = j < n_act;
-        const bool act_next = j + 1 < n_act;
-        f16x8 kf[T::NB][T::KK];
-        f16x8 vf[T::NB][2][T::DB];
-        if (act_next) load_k_frags<T>(kb[(j + 1) % NBUF], fr, kf);
-        if (act) load_v_frags<T>(vb[j % NBUF], fr, vf);
-        if (j + 2 < n_tiles) load_tile<T>(kh, (j + 2) * T::BC, n, kb[(j + 2) % NBUF], dma);
-        if (j + 1 < n_tiles) load_tile<T>(vh, (j + 1) * T::BC, n, vb[(j + 1) % NBUF], dma);
-        if (!act) continue;  // wave-uniform: fully masked for this wave (causal)
-        f32x16 s2[T::NB];
-        if (act_next) {
-#pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb) {
-                s2[nb] = f32x16{};
-#pragma unroll
-                for (int kk = 0; kk < T::KK; ++kk) s2[nb] = mfma32(kf[nb][kk], qf[kk], s2[nb]);
-            }
-        }
-        const int kt = j * T::BC;
-        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
-        f16x8 p[T::NB][2];
-        float alpha;
-        bool rescale;
-        softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale_o<T>(oacc, alpha);
-        pv_frags<T>(vf, p, oacc);
-        if (act_next) {
-#pragma unroll
-            for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
-        }
-    }
-}
-
-// ---- kernel, software-pipelined schedule ----------------------------------
-// Each wave overlaps the S^T = K Q^T MFMAs of tile j+1 with the softmax VALU work of tile j in
-// one straight-line block, then issues tile j's P.V MFMAs; with two waves per SIMD the matrix
-// pipe is fed while either wave is in its softmax. K and V are double-buffered separately:
-// at the barrier of iteration j, K_{j+2} and V_{j+1} are requested (their buffers were last
-// read by QK_j and PV_{j-1}, both finished before that barrier), and both land before the
-// next barrier. Tiles run in two loops: a steady-state loop over tiles that need no mask and
-// whose successor is visible to the wave, and a general loop for the rest (diagonal and tail
-// tiles, and tiles a causal wave only waits through).
-template <class T, bool CAUSAL>
-__global__ __launch_bounds__(T::THREADS) void flash_fwd_pipelined(
-    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
-    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
-    float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
-    float* /*lse_part*/) {
-    // Four separate LDS objects (K and V, two buffers each): with the buffer known at compile
-    // time, the compiler can tell that a DMA refill and a fragment read touch different
-    // objects and adds no wait between them.
-    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = wave_uniform(threadIdx.x >> 6);
-    const g::Work w = g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
-    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
-    const f16* kh = k + head;
-    const f16* vh = v + head;
-    const int q0 = w.qb * T::BR;
-    const int qw = q0 + wave * 32;
-    const int qrow = qw + (lane & 31);
-    const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-    // Tiles this wave computes (the rest it only waits through), and the leading run of them
-    // that needs no masking.
-    const int n_act = g::wave_active_tiles(n, qw, 32, T::BC, n_tiles, CAUSAL);
-    const int n_plain = g::wave_unmasked_tiles(n, qw, T::BC, n_act, CAUSAL);
-
-    auto kbuf = [&](int b) { return b ? k_lds1 : k_lds0; };
-    auto vbuf = [&](int b) { return b ? v_lds1 : v_lds0; };
-
-    const TileDma<T> dma(wave, lane);
-    load_tile<T>(kh, 0, n, kbuf(0), dma);
-    load_tile<T>(vh, 0, n, vbuf(0), dma);
-    if (n_tiles > 1) load_tile<T>(kh, T::BC, n, kbuf(1), dma);
-    f16x8 qf[T::KK];
-    load_q<T>(q + head, qrow, n, lane, negate_q, qf);
-    const Frag<T> fr(lane);
-
-    f32x16 oacc[T::DB];
-#pragma unroll
-    for (int db = 0; db < T::DB; ++db) oacc[db] = f32x16{};
-    float m_run = -INFINITY;
-    float l_run = 0.0F;
-
-    wait_vmem();
-    __syncthreads();
-    f32x16 s[T::NB];
-    f32x16 s2[T::NB];
-    if (n_act > 0) qk_tile<T>(kbuf(0), fr, qf, s);
-
-    // Steady state: tile j unmasked, tile j+1 active. Right after the barrier the refill is
-    // requested (K_{j+2} into K buffer j%2, V_{j+1} into V buffer (j+1)%2; both buffers were
-    // last read before this barrier), so it has a whole iteration to land; it is
-    // unconditional so it shares the scheduling region, and a K tile past the end reads as
-    // zeros into a buffer nobody reads again. The fragment reads of this iteration (K of tile
-    // j+1, V^T of tile j) touch the other LDS objects, so they need not wait for it. The QK MFMAs of tile j+1 are interleaved with tile j's
-    // softmax (sched_steady_region); then, after the rarely taken rescale branch, tile j's PV
-    // MFMAs. Two tiles per trip, so every buffer address is an immediate and the score
-    // registers alternate between s and s2 without copies.
-    auto steady = [&](int jj, auto parity, f32x16(&s_cur)[T::NB], f32x16(&s_nxt)[T::NB]) {
-        constexpr int PAR = decltype(parity)::value;  // jj % 2
-        wait_vmem();
-        __syncthreads();
-        load_tile<T>(kh, (jj + 2) * T::BC, n, kbuf(PAR), dma);
-        load_tile<T>(vh, (jj + 1) * T::BC, n, vbuf(1 - PAR), dma);
-        f16x8 kf[T::NB][T::KK];
-        load_k_frags<T>(kbuf(1 - PAR), fr, kf);
-        f16x8 vf[T::NB][2][T::DB];
-        load_v_frags<T>(vbuf(PAR), fr, vf);
-        f16x8 p[T::NB][2];
-        float alpha;
-        bool rescale;
-        if constexpr (T::LAZY && FA_OPTIMISTIC) {
-            bool overflow;
-            qk_softmax_optimistic<T>(kf, qf, s_cur, scale_log2, m_run, l_run, overflow, s_nxt,
-                                     p);
-            sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
-                                2 * T::DMA_ITERS, T::NB * T::KK>();
-            if (overflow) {  // rare: the exact softmax of this tile, new max, rescaled O
-                softmax_tile<T>(s_cur, scale_log2, m_run, l_run, alpha, rescale, p);
-                if (rescale) rescale_o<T>(oacc, alpha);
-            }
-        } else {
-            qk_softmax_interleaved<T>(kf, qf, s_cur, scale_log2, m_run, l_run, alpha, rescale,
-                                      s_nxt, p);
-            sched_steady_region<FA_VALU_PER_MFMA, T::NB * T::KK, T::NB * 4 * T::DB,
-                                2 * T::DMA_ITERS, T::NB * T::KK>();
-            if (rescale) rescale_o<T>(oacc, alpha);
-        }
-        pv_frags<T>(vf, p, oacc);
-    };
-    const int n_steady = min(n_plain, n_act - 1);
-    int j = 0;
-    for (; j + 2 <= n_steady; j += 2) {
-        steady(j, std::integral_constant<int, 0>{}, s, s2);
-        steady(j + 1, std::integral_constant<int, 1>{}, s2, s);
-    }
-    if (j < n_steady) {
-        steady(j, std::integral_constant<int, 0>{}, s, s2);
-#pragma unroll
-        for (int nb = 0; nb < T::NB; ++nb) s[nb] = s2[nb];
-        ++j;
-    }
-
-    char* kb[2];
-    char* vb[2];
-    kb[0] = k_lds0;
-    kb[1] = k_lds1;
-    vb[0] = v_lds0;
-    vb[1] = v_lds1;
-    general_tiles<T, CAUSAL, 2>(j, n_tiles, n_act, n, qw, qrow, lane, kh, vh, kb, vb, dma, fr, qf, s,
-                                oacc, scale_log2, m_run, l_run);
-    store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
-               m_run, l_run, oacc);
 }
 
 // ---- ping-pong schedule: phase protocol ---------------------------------------------------------
@@ -1473,7 +1124,7 @@ __device__ __forceinline__ void store16_partial(float* op, float* lp, int qw, in
     }
 }
 
-// Tiles j .. n_tiles-1 outside the steady phases (as general_tiles): one barrier each; K_t
+// Tiles j .. n_tiles-1 outside the steady phases: one barrier each; K_t
 // and V_t in buffer t % 3; refills of K_{j+2} and V_{j+1}.
 template <class T, bool CAUSAL>
 __device__ __forceinline__ void general_tiles16(
@@ -1742,16 +1393,20 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
 // (csrc/kernels/flash_fwd.cu:597-612). On MI355X the best tile also depends on the sequence
-// length, so the "opt" / "fp16acc" rows are split by N at thresholds found by the tile sweep
-// (FA2-paper shapes, B*N = 16k tokens): short sequences favour 256-row workgroups with the
-// simple schedule (less pipeline prologue and epilogue per workgroup, fewer diagonal tiles
-// on the ping-pong's masked path), long ones the ping-pong or pipelined schedules. Small grids
-// (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000) take the key-split
-// schedule with 64-row workgroups: two waves per 32 query rows, each on half the key tiles,
-// so the same grid keeps twice the SIMDs busy. Each entry is
-// "BC, NW, LAZY, SCHED" and can be overridden at build time with -DFA_<NAME>="..." (the
-// counterpart of bench/tune.sh, which rewrites the `using` lines with sed); so can each
-// threshold (a row applies while N <= its FA_*_MAX_N).
+// length and the grid size, so the "opt" / "fp16acc" rows are split by N at thresholds found by
+// the tile sweep (FA2-paper shapes, B*N = 16k tokens):
+//   * d = 64: the 8-wave simple schedule at every length (256-row workgroups, 64-key tiles, two
+//     workgroups per CU); with the optimistic softmax its VALU work per tile is low enough that
+//     the four waves per SIMD keep the matrix pipe busier than the ping-pong does;
+//   * d = 128: the 16x16x32 ping-pong for long sequences; below a threshold the 4-wave simple
+//     tile, which has no pipeline prologue and epilogue per workgroup (and, when causal, fewer
+//     diagonal tiles);
+//   * small grids (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000): the
+//     key-split schedule with 64-row workgroups (two waves per 32 query rows, each on half the
+//     key tiles), so the same grid keeps twice the SIMDs busy.
+// Each entry is "BC, NW, LAZY, SCHED" and can be overridden at build time with
+// -DFA_<NAME>="..." (the counterpart of bench/tune.sh, which rewrites the `using` lines with
+// sed); so can each threshold (a row applies while N <= its FA_*_MAX_N).
 #ifndef FA_BASE_D64
 #define FA_BASE_D64 64, 4, false, SIMPLE
 #endif
@@ -1764,20 +1419,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #ifndef FA_OPT_D128_SMALL
 #define FA_OPT_D128_SMALL 32, 2, true, KSPLIT
 #endif
-#ifndef FA_OPT_D64_SHORT
-#define FA_OPT_D64_SHORT 64, 8, true, SIMPLE
-#endif
 #ifndef FA_OPT_D64
-#define FA_OPT_D64 64, 8, true, PINGPONG16
-#endif
-#ifndef FA_OPT_D64_CAUSAL_SHORT
-#define FA_OPT_D64_CAUSAL_SHORT 64, 8, true, SIMPLE
+#define FA_OPT_D64 64, 8, true, SIMPLE
 #endif
 #ifndef FA_OPT_D64_CAUSAL
-#define FA_OPT_D64_CAUSAL 32, 4, true, PIPE
+#define FA_OPT_D64_CAUSAL 64, 8, true, SIMPLE
 #endif
-#ifndef FA_OPT_D64_CAUSAL_LONG
-#define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG16
+#ifndef FA_OPT_D128_SHORT
+#define FA_OPT_D128_SHORT 32, 4, true, SIMPLE
 #endif
 #ifndef FA_OPT_D128
 #define FA_OPT_D128 32, 8, true, PINGPONG16
@@ -1788,14 +1437,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #ifndef FA_OPT_D128_CAUSAL
 #define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG16
 #endif
-#ifndef FA_D64_SHORT_MAX_N
-#define FA_D64_SHORT_MAX_N 2048
-#endif
-#ifndef FA_D64_CAUSAL_SHORT_MAX_N
-#define FA_D64_CAUSAL_SHORT_MAX_N 4096
-#endif
-#ifndef FA_D64_CAUSAL_MAX_N
-#define FA_D64_CAUSAL_MAX_N 8192
+#ifndef FA_D128_SHORT_MAX_N
+#define FA_D128_SHORT_MAX_N 1024
 #endif
 #ifndef FA_D128_CAUSAL_SHORT_MAX_N
 #define FA_D128_CAUSAL_SHORT_MAX_N 2048
@@ -1813,8 +1456,7 @@ struct Entry {
 enum TileId : int {
     BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
     OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
-    OPT_D64_SHORT, OPT_D64, OPT_D64_C_SHORT, OPT_D64_C, OPT_D64_C_LONG,
-    OPT_D128, OPT_D128_C_SHORT, OPT_D128_C,
+    OPT_D64, OPT_D64_C, OPT_D128_SHORT, OPT_D128, OPT_D128_C_SHORT, OPT_D128_C,
 };
 template <int ID> struct Row;
 template <> struct Row<BASE_D64> : Entry<Tile<64, FA_BASE_D64>, false> {};
@@ -1825,11 +1467,9 @@ template <> struct Row<OPT_D64_SMALL> : Entry<Tile<64, FA_OPT_D64_SMALL>, false>
 template <> struct Row<OPT_D64_C_SMALL> : Entry<Tile<64, FA_OPT_D64_SMALL>, true> {};
 template <> struct Row<OPT_D128_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, false> {};
 template <> struct Row<OPT_D128_C_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, true> {};
-template <> struct Row<OPT_D64_SHORT> : Entry<Tile<64, FA_OPT_D64_SHORT>, false> {};
 template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
-template <> struct Row<OPT_D64_C_SHORT> : Entry<Tile<64, FA_OPT_D64_CAUSAL_SHORT>, true> {};
 template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
-template <> struct Row<OPT_D64_C_LONG> : Entry<Tile<64, FA_OPT_D64_CAUSAL_LONG>, true> {};
+template <> struct Row<OPT_D128_SHORT> : Entry<Tile<128, FA_OPT_D128_SHORT>, false> {};
 template <> struct Row<OPT_D128> : Entry<Tile<128, FA_OPT_D128>, false> {};
 template <> struct Row<OPT_D128_C_SHORT> : Entry<Tile<128, FA_OPT_D128_CAUSAL_SHORT>, true> {};
 template <> struct Row<OPT_D128_C> : Entry<Tile<128, FA_OPT_D128_CAUSAL>, true> {};
@@ -1844,12 +1484,8 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
         if (head_dim == 64) return causal ? OPT_D64_C_SMALL : OPT_D64_SMALL;
         return causal ? OPT_D128_C_SMALL : OPT_D128_SMALL;
     }
-    if (head_dim == 64) {
-        if (!causal) return n <= FA_D64_SHORT_MAX_N ? OPT_D64_SHORT : OPT_D64;
-        if (n <= FA_D64_CAUSAL_SHORT_MAX_N) return OPT_D64_C_SHORT;
-        return n <= FA_D64_CAUSAL_MAX_N ? OPT_D64_C : OPT_D64_C_LONG;
-    }
-    if (!causal) return OPT_D128;
+    if (head_dim == 64) return causal ? OPT_D64_C : OPT_D64;
+    if (!causal) return n <= FA_D128_SHORT_MAX_N ? OPT_D128_SHORT : OPT_D128;
     return n <= FA_D128_CAUSAL_SHORT_MAX_N ? OPT_D128_C_SHORT : OPT_D128_C;
 }
 
@@ -1865,11 +1501,9 @@ decltype(auto) with_row(TileId id, F&& f) {
         case OPT_D64_C_SMALL: return f(Row<OPT_D64_C_SMALL>{});
         case OPT_D128_SMALL: return f(Row<OPT_D128_SMALL>{});
         case OPT_D128_C_SMALL: return f(Row<OPT_D128_C_SMALL>{});
-        case OPT_D64_SHORT: return f(Row<OPT_D64_SHORT>{});
         case OPT_D64: return f(Row<OPT_D64>{});
-        case OPT_D64_C_SHORT: return f(Row<OPT_D64_C_SHORT>{});
         case OPT_D64_C: return f(Row<OPT_D64_C>{});
-        case OPT_D64_C_LONG: return f(Row<OPT_D64_C_LONG>{});
+        case OPT_D128_SHORT: return f(Row<OPT_D128_SHORT>{});
         case OPT_D128: return f(Row<OPT_D128>{});
         case OPT_D128_C_SHORT: return f(Row<OPT_D128_C_SHORT>{});
         default: return f(Row<OPT_D128_C>{});
@@ -1938,8 +1572,6 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL>);
     } else if constexpr (T::SCHED == KSPLIT) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
-    } else if constexpr (T::SCHED == PIPE) {
-        fn = reinterpret_cast<const void*>(&flash_fwd_pipelined<T, CAUSAL>);
     } else {
         fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL>);
     }
@@ -1979,16 +1611,17 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15U
 #ifndef FA_SPLIT_PLAN_D128_CAUSAL
 #define FA_SPLIT_PLAN_D128_CAUSAL 512, 1024
 #endif
-template <class T_, int TARGET_WGS_, int MIN_KEYS_>
+template <class T_, bool CAUSAL_, int TARGET_WGS_, int MIN_KEYS_>
 struct SplitRow {
     using T = T_;
+    static constexpr bool CAUSAL = CAUSAL_;
     static constexpr int TARGET_WGS = TARGET_WGS_;
     static constexpr int MIN_KEYS = MIN_KEYS_;
 };
-using SplitD64 = SplitRow<Tile<64, FA_SPLIT_D64>, FA_SPLIT_PLAN>;
-using SplitD64C = SplitRow<Tile<64, FA_SPLIT_D64_CAUSAL>, FA_SPLIT_PLAN_D64_CAUSAL>;
-using SplitD128 = SplitRow<Tile<128, FA_SPLIT_D128>, FA_SPLIT_PLAN>;
-using SplitD128C = SplitRow<Tile<128, FA_SPLIT_D128_CAUSAL>, FA_SPLIT_PLAN_D128_CAUSAL>;
+using SplitD64 = SplitRow<Tile<64, FA_SPLIT_D64>, false, FA_SPLIT_PLAN>;
+using SplitD64C = SplitRow<Tile<64, FA_SPLIT_D64_CAUSAL>, true, FA_SPLIT_PLAN_D64_CAUSAL>;
+using SplitD128 = SplitRow<Tile<128, FA_SPLIT_D128>, false, FA_SPLIT_PLAN>;
+using SplitD128C = SplitRow<Tile<128, FA_SPLIT_D128_CAUSAL>, true, FA_SPLIT_PLAN_D128_CAUSAL>;
 
 template <class F>
 auto with_split_row(int head_dim, bool causal, F&& f) {
@@ -2079,17 +1712,15 @@ int combine(const fa_params& p, const SplitPlan& sp, const float* o_part, const 
     return FA_OK;
 }
 
-template <class T>
+template <class R>
 int splitkv(const fa_params& p, float* lse, const SplitPlan& sp, void* workspace, Scale sc,
             hipStream_t stream) {
+    using T = typename R::T;
     auto* o_part = static_cast<float*>(workspace);
     float* lse_part = o_part + static_cast<size_t>(sp.n_splits) * p.batch * p.heads * p.seqlen *
                                    T::D;
-    const int rc = p.causal
-                       ? launch<T, true, true>(p, nullptr, stream, sc, sp.n_splits,
-                                               sp.tiles_per_split, o_part, lse_part)
-                       : launch<T, false, true>(p, nullptr, stream, sc, sp.n_splits,
-                                                sp.tiles_per_split, o_part, lse_part);
+    const int rc = launch<T, R::CAUSAL, true>(p, nullptr, stream, sc, sp.n_splits,
+                                              sp.tiles_per_split, o_part, lse_part);
     if (rc != FA_OK) return rc;
     return combine<T::D>(p, sp, o_part, lse_part, lse, stream);
 }
@@ -2277,7 +1908,7 @@ static int splitkv_run(const fa_params& p, float* lse, const fa::SplitPlan& sp, 
     const fa::Scale sc = fa::scale_of(p.softmax_scale);
     auto s = static_cast<hipStream_t>(stream);
     return fa::with_split_row(p.head_dim, p.causal != 0, [&](auto row) {
-        return fa::splitkv<typename decltype(row)::T>(p, lse, sp, workspace, sc, s);
+        return fa::splitkv<decltype(row)>(p, lse, sp, workspace, sc, s);
     });
 }
 

@@ -7,12 +7,11 @@
             [--reps 3] [--csv PATH] [--bh B H] [--dev-args "--std 0.5 --boost-keys 0.01:8"]
 
 slot: one row of the tile table in csrc/flash_fwd.hip, named after its macro (see SLOTS):
-      opt_d64[_causal]_small, opt_d128[_causal]_small, opt_d64_short, opt_d64,
-      opt_d64_causal_short, opt_d64_causal, opt_d64_causal_long, opt_d128,
-      opt_d128_causal_short, opt_d128_causal, base_d64, base_d128
+      opt_d64[_causal]_small, opt_d128[_causal]_small, opt_d64, opt_d64_causal,
+      opt_d128_short, opt_d128, opt_d128_causal_short, opt_d128_causal, base_d64, base_d128
 cand: "BC,NW,LAZY,SCHED" -- keys per tile, query waves per workgroup (BR = 32 * NW), lazy
-      rescale (true/false) and schedule (SIMPLE, PIPE, KSPLIT, which runs two waves per query
-      wave, or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128, BC=64 at
+      rescale (true/false) and schedule (SIMPLE; KSPLIT, which runs two waves per query wave;
+      or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128, BC=64 at
       D=64), e.g. 32,8,true,PINGPONG16. Without candidates a default list for the slot is used.
 
 `build` compiles csrc/flash_fwd.hip once per candidate with the slot's macro overridden, into
@@ -56,17 +55,10 @@ SLOTS = {
     "opt_d128_small": ("FA_OPT_D128_SMALL", "opt", 128, 0, [f"-DFA_SMALL_GRID_WGS={_ALL}"]),
     "opt_d128_causal_small": ("FA_OPT_D128_SMALL", "opt", 128, 1,
                               [f"-DFA_SMALL_GRID_WGS={_ALL}"]),
-    "opt_d64_short": ("FA_OPT_D64_SHORT", "opt", 64, 0, [*_BIG, f"-DFA_D64_SHORT_MAX_N={_ALL}"]),
-    "opt_d64": ("FA_OPT_D64", "opt", 64, 0, [*_BIG, f"-DFA_D64_SHORT_MAX_N={_NONE}"]),
-    "opt_d64_causal_short": ("FA_OPT_D64_CAUSAL_SHORT", "opt", 64, 1,
-                             [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_ALL}"]),
-    "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1,
-                       [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_NONE}",
-                        f"-DFA_D64_CAUSAL_MAX_N={_ALL}"]),
-    "opt_d64_causal_long": ("FA_OPT_D64_CAUSAL_LONG", "opt", 64, 1,
-                            [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_NONE}",
-                             f"-DFA_D64_CAUSAL_MAX_N={_NONE}"]),
-    "opt_d128": ("FA_OPT_D128", "opt", 128, 0, _BIG),
+    "opt_d64": ("FA_OPT_D64", "opt", 64, 0, _BIG),
+    "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1, _BIG),
+    "opt_d128_short": ("FA_OPT_D128_SHORT", "opt", 128, 0, [*_BIG, f"-DFA_D128_SHORT_MAX_N={_ALL}"]),
+    "opt_d128": ("FA_OPT_D128", "opt", 128, 0, [*_BIG, f"-DFA_D128_SHORT_MAX_N={_NONE}"]),
     "opt_d128_causal_short": ("FA_OPT_D128_CAUSAL_SHORT", "opt", 128, 1,
                               [*_BIG, f"-DFA_D128_CAUSAL_SHORT_MAX_N={_ALL}"]),
     "opt_d128_causal": ("FA_OPT_D128_CAUSAL", "opt", 128, 1,
@@ -75,11 +67,10 @@ SLOTS = {
     "base_d128": ("FA_BASE_D128", "base", 128, 0, []),
 }
 DEFAULT_CANDS = {
-    64: ["32,4,true,PIPE", "64,4,true,PIPE", "64,8,true,PINGPONG16", "32,4,true,SIMPLE",
-         "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "64,2,true,KSPLIT",
-         "32,2,true,KSPLIT"],
-    128: ["32,8,true,PINGPONG16", "32,8,true,PIPE", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "32,2,true,KSPLIT",
-          "32,4,true,KSPLIT"],
+    64: ["64,8,true,PINGPONG16", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE",
+         "64,4,false,SIMPLE", "64,2,true,KSPLIT", "32,2,true,KSPLIT"],
+    128: ["32,8,true,PINGPONG16", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE",
+          "64,4,false,SIMPLE", "32,2,true,KSPLIT", "32,4,true,KSPLIT"],
 }
 
 

@@ -121,15 +121,13 @@ def test_tile_config_invariants():
 
 def test_tile_config_rows():
     """The opt rows by N for a large grid (16 x 32 heads), and the small-grid rows."""
-    pingpong64, simple64x8 = (256, 64, 8, 49152), (256, 64, 8, 32768)
-    assert _tile(64, False, "opt", 2048) == simple64x8
-    assert _tile(64, False, "opt", 2049) == pingpong64
-    assert _tile(64, True, "opt", 4096) == simple64x8
-    assert _tile(64, True, "opt", 4097) == (128, 32, 4, 16384)         # pipelined
-    assert _tile(64, True, "opt", 8192) == (128, 32, 4, 16384)
-    assert _tile(64, True, "opt", 8193) == pingpong64
-    assert _tile(128, False, "opt", 512) == (256, 32, 8, 49152)        # ping-pong at every N
-    assert _tile(128, True, "opt", 2048) == (128, 32, 4, 32768)        # simple, 4 waves
+    simple64x8, simple128x4 = (256, 64, 8, 32768), (128, 32, 4, 32768)
+    for n in (1, 2048, 4097, 8193, 16384):                             # d=64: one row
+        assert _tile(64, False, "opt", n) == simple64x8
+        assert _tile(64, True, "opt", n) == simple64x8
+    assert _tile(128, False, "opt", 1024) == simple128x4
+    assert _tile(128, False, "opt", 1025) == (256, 32, 8, 49152)       # ping-pong
+    assert _tile(128, True, "opt", 2048) == simple128x4
     assert _tile(128, True, "opt", 2049) == (256, 32, 8, 49152)
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
     # two waves on each 32 rows)

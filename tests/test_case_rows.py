@@ -1,0 +1,66 @@
+"""CPU: the GPU tests' shape lists reach the tile rows they are meant to cover.
+
+fa_tile_config runs on the host, so the row each GPU case selects is checked here, before any
+GPU run: every expected tile of the row and switch tests, the ping-pong cases, the large-grid
+edge lengths, and full coverage of the opt rows by the NaN-prefilled-O shapes and the row
+tests (each (head_dim, causal, tile) combination the table can pick).
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from fa import native
+
+import test_forward_routing as routing
+import test_lse_splitkv as lse_cases
+import test_tile_rows as rows
+
+
+def _tile(b, h, n, d, causal, variant="opt"):
+    t = native.tile_config(d, causal, variant, n, b, h)
+    return t["block_q"], t["block_k"], t["waves"], t["lds_bytes"]
+
+
+# Every (head_dim, causal, tile) the opt table can pick: the key split for small grids, the
+# simple tile, and at d=128 the ping-pong.
+OPT_ROWS = {
+    (64, False, rows.SMALL64), (64, True, rows.SMALL64),
+    (64, False, rows.SIMPLE64X8), (64, True, rows.SIMPLE64X8),
+    (128, False, rows.SMALL128), (128, True, rows.SMALL128),
+    (128, False, rows.SIMPLE128X4), (128, True, rows.SIMPLE128X4),
+    (128, False, rows.PP128), (128, True, rows.PP128),
+}
+
+
+@pytest.mark.parametrize("b,h,n,d,causal,want", rows.ROWS + rows.SWITCHES)
+def test_row_cases_select_their_tile(b, h, n, d, causal, want):
+    assert _tile(b, h, n, d, causal) == want
+
+
+def test_row_cases_cover_every_opt_row():
+    assert {(d, c, w) for _, _, _, d, c, w in rows.ROWS} == OPT_ROWS
+
+
+def test_pingpong_cases_select_the_pingpong():
+    for b, h, n, causal in rows.PP_SCALE_CASES:
+        assert _tile(b, h, n, 128, causal) == rows.PP128
+
+
+@pytest.mark.parametrize("n", [1, 17, 65, 257, 1000])
+def test_edge_lengths_stay_off_the_small_grid_row(n):
+    for d in (64, 128):
+        for causal in (False, True):
+            assert _tile(16, 16, n, d, causal)[0] in (128, 256)
+
+
+def test_tail_shapes_cover_every_opt_row():
+    got = {(d, c, _tile(b, h, n, d, c)) for b, h, n, d, c, var in routing.TAIL_SHAPES
+           if var == "opt"}
+    assert got == OPT_ROWS
+
+
+def test_lse_cases_cover_every_kind_of_tile():
+    got = {_tile(b, h, n, d, c) for b, h, n, d, c in lse_cases.LSE_CASES}
+    want = {w for _, _, w in OPT_ROWS}
+    assert got == want

@@ -19,7 +19,7 @@ import pytest
 RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" / "fa" / \
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
-SIMPLE, PIPE, KSPLIT, PINGPONG16 = 0, 1, 3, 4
+SIMPLE, KSPLIT, PINGPONG16 = 0, 3, 4
 # flash_fwd_kernel<Tile, CAUSAL, SPLIT>: the split-KV build ends its template arguments in Lb1E
 SPLIT_SUFFIX_RE = re.compile(r"ELb[01]ELb1EEEv")
 
@@ -30,24 +30,6 @@ def _load():
     return json.loads(RES.read_text())
 
 
-def _min_occupancy(name: str) -> int:
-    if "flash_fwd_combine" in name:
-        return 4
-    d, bc, nw, _lazy, sched = (int(x) for x in TILE.search(name).groups())
-    if "flash_fwd_pingpong16" in name:
-        return 2                      # waves w and w+4 share a SIMD
-    if "flash_fwd_ksplit" in name:
-        return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
-    if "flash_fwd_pipelined" in name:
-        return 3 if d == 64 else 1
-    assert "flash_fwd_kernel" in name and sched == SIMPLE
-    if SPLIT_SUFFIX_RE.search(name) and d == 64:
-        # the split-KV partial pass of causal d=64 (4-wave tile): its extra range bookkeeping
-        # takes it to 148 VGPRs, three waves per SIMD, measured as fast as the four-wave build
-        return 3
-    return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
-
-
 def _family(mangled: str) -> str:
     """Kernel function name of a mangled symbol (_ZN2fa12_GLOBAL__N_1<len><name>I...)."""
     m = re.search(r"_GLOBAL__N_1(\d+)", mangled)
@@ -56,10 +38,27 @@ def _family(mangled: str) -> str:
     return mangled[start:start + int(m.group(1))]
 
 
+def _min_occupancy(name: str) -> int:
+    family = _family(name)
+    if family == "flash_fwd_combine":
+        return 4
+    d, bc, nw, _lazy, sched = (int(x) for x in TILE.search(name).groups())
+    if family == "flash_fwd_pingpong16":
+        return 2                      # waves w and w+4 share a SIMD
+    if family == "flash_fwd_ksplit":
+        return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
+    assert family == "flash_fwd_kernel" and sched == SIMPLE, name
+    if SPLIT_SUFFIX_RE.search(name) and d == 64:
+        # the split-KV partial pass of causal d=64 (4-wave tile): its extra range bookkeeping
+        # takes it to 148 VGPRs, three waves per SIMD, measured as fast as the four-wave build
+        return 3
+    return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
+
+
 def test_every_kernel_is_recorded():
     families = {_family(k) for k in _load()}
-    assert families == {"flash_fwd_kernel", "flash_fwd_pingpong16", "flash_fwd_pipelined",
-                        "flash_fwd_ksplit", "flash_fwd_combine"}, families
+    assert families == {"flash_fwd_kernel", "flash_fwd_pingpong16", "flash_fwd_ksplit",
+                        "flash_fwd_combine"}, families
 
 
 def test_no_kernel_spills_to_scratch():

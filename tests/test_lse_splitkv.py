@@ -36,11 +36,11 @@ def _slices(b, h):
     return [(slice(bi, bi + 1), slice(hi, hi + 1)) for bi, hi in {(0, 0), (b - 1, h - 1)}]
 
 
-# Shapes that reach every kind of tile row (small grid, simple, pipelined, ping-pong).
+# Shapes that reach every kind of tile row (small grid, simple, ping-pong).
 LSE_CASES = [
     (2, 3, 257, 64, False), (2, 3, 1000, 128, True),      # small grids
-    (4, 16, 1000, 64, True), (4, 16, 1000, 128, False),   # simple / ping-pong, large grid
-    (1, 16, 5000, 64, True), (1, 32, 2500, 64, False),    # pipelined / ping-pong d=64
+    (4, 16, 1000, 64, True), (4, 16, 1000, 128, False),   # simple 8 and 4 waves, large grid
+    (1, 16, 5000, 64, True), (2, 16, 2500, 128, False),   # simple d=64 long / ping-pong d=128
     (1, 16, 4000, 128, True),                             # ping-pong causal
 ]
 

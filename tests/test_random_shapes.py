@@ -2,7 +2,7 @@
 
 Forty draws (fixed seed, so the case list is the same on every run) of batch, heads, sequence
 length, head dim, causal, variant and softmax scale, with B*H*N small enough for the oracle but
-spread so that every tile row (small grid, simple, pipelined, ping-pong, key split) and both
+spread so that every tile row (small grid key split, simple, ping-pong) and both
 sides of the size thresholds come up. Each case checks fa.forward_variant against the fp32
 oracle on two (b, h) slices with the north-star tolerance, and fa.forward_lse's LSE against the
 oracle's LSE (2e-3 absolute).
