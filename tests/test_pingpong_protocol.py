@@ -1,4 +1,4 @@
-"""CPU: the K/V buffer protocol of the ping-pong kernel (csrc/flash_fwd.hip, flash_fwd_pingpong).
+"""CPU: the K/V buffer protocol of the ping-pong kernel (csrc/flash_fwd.hip, flash_fwd_pingpong16).
 
 The kernel's steady state is a sequence of global phases separated by workgroup barriers.
 Group 0 runs the softmax phase S_j in phase 2j and the matrix phase M_j in 2j+1; group 1 runs
@@ -6,12 +6,12 @@ one phase later (its M_{-1}, phase 0, only issues requests). K_t and V_t live in
 t mod 3. S_j reads the K_{j+1} and V_j fragments; in M_j group 0 requests K_{j+3} and V_{j+2},
 group 1 requests K_{j+4} and V_{j+3}; at the end of every odd phase each wave waits until at
 most its two newest requests are in flight (vmcnt(2)). The prologue leaves K_0, K_1, K_2, V_0
-and V_1 resident, and general_tiles takes over at tile n_steady after a full wait.
+and V_1 resident, and general_tiles16 takes over at tile n_steady after a full wait.
 
 This model replays that schedule for every steady length and checks what the kernel relies on:
 each fragment read finds its tile landed, no request is in flight into a buffer some wave reads
 in the same phase, two requests for different tiles never overlap in one buffer, and the state
-handed to general_tiles is the one it expects.
+handed to general_tiles16 is the one it expects.
 """
 
 from __future__ import annotations
@@ -55,7 +55,7 @@ def simulate(n_steady: int) -> dict:
                 for (_, buf, tile) in pending[g][:-2]:
                     landed[buf] = tile
                 pending[g] = pending[g][-2:]
-    for g in (0, 1):  # general_tiles starts with a full wait
+    for g in (0, 1):  # general_tiles16 starts with a full wait
         for (_, buf, tile) in pending[g]:
             landed[buf] = tile
     return landed
@@ -64,7 +64,7 @@ def simulate(n_steady: int) -> dict:
 @pytest.mark.parametrize("n_steady", list(range(1, 40)))
 def test_protocol_invariants(n_steady):
     landed = simulate(n_steady)
-    # general_tiles at j0 = n_steady reads K_{j0+1} and V_{j0}
+    # general_tiles16 at j0 = n_steady reads K_{j0+1} and V_{j0}
     assert landed[("k", (n_steady + 1) % 3)] == n_steady + 1
     assert landed[("v", n_steady % 3)] == n_steady
 
