@@ -714,6 +714,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
 // or 4 phases before its first read, and replaces a tile whose last read was in an earlier
 // phase. Diagonal and tail tiles are masked inside the steady phases; only the last tile, which
 // has no successor to prefetch, goes through general_tiles16 afterwards.
+// Causal ping-pong grids of workgroups that each run a (long, short) pair of query blocks.
+#ifndef FA_CAUSAL_PAIRS
+#define FA_CAUSAL_PAIRS 1
+#endif
 // Wave priorities (s_setprio) of the ping-pong's matrix phase and softmax phase.
 #ifndef FA_PP_PRIO
 #define FA_PP_PRIO 1
@@ -1187,6 +1191,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
+    constexpr bool PAIRED = CAUSAL && !SPLIT && FA_CAUSAL_PAIRS;
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1199,9 +1204,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int grp = wave >> 2;
     const int items = bh_count * n_qblocks;
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
-    const g::Work w = SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
-                                         n_qblocks, CAUSAL)
-                            : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    // One (head, query block) item: the whole single-item kernel.
+    auto run_item = [&](const g::Work w) {
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const int q0 = w.qb * T::BR;
     const int qw = q0 + wave * 32;  // first query of this wave (Q loads, O stores)
@@ -1388,6 +1392,22 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
                    m_run, l_run, oacc);
     }
+    };
+    if constexpr (PAIRED) {
+        // Causal grids: each workgroup runs the pair of query blocks (long, short) =
+        // (n_qblocks - 1 - p, p), so that every workgroup has the same number of tiles
+        // (fa::geom::causal_pair).
+        const g::PairWork pw = g::causal_pair(static_cast<int>(blockIdx.x), bh_count, n_qblocks);
+        run_item(g::Work{pw.bh, pw.qb_long});
+        if (pw.qb_short >= 0) {
+            __syncthreads();  // the first item's last LDS reads, before the second item's DMA
+            run_item(g::Work{pw.bh, pw.qb_short});
+        }
+    } else {
+        run_item(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                                    n_qblocks, CAUSAL)
+                       : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
+    }
 }
 
 // ---- tile table -------------------------------------------------------------------------------
@@ -1557,8 +1577,8 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
     int negate_q = sc.negate_q;
     void* args[] = {&qp, &kp, &vp, &op, &lse, &n, &bh, &nqb, &scale_log2, &negate_q,
                     &tiles_per_split, &o_part, &lse_part};
-    const dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh) *
-                    static_cast<unsigned>(n_splits));
+    dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh) *
+              static_cast<unsigned>(n_splits));
     const void* fn;
     if constexpr (SPLIT) {
         static_assert(T::SCHED == SIMPLE || T::SCHED == PINGPONG16,
@@ -1569,6 +1589,9 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
             fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
         }
     } else if constexpr (T::SCHED == PINGPONG16) {
+        if constexpr (CAUSAL && FA_CAUSAL_PAIRS) {
+            grid = dim3(static_cast<unsigned>(bh) * static_cast<unsigned>((n_qblocks + 1) / 2));
+        }
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL>);
     } else if constexpr (T::SCHED == KSPLIT) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);

@@ -53,6 +53,13 @@ void geom_work_of_xcd(int block_id, int bh_count, int n_qblocks, int causal, int
     *bh = w.bh;
     *qb = w.qb;
 }
+void geom_causal_pair(int block_id, int bh_count, int n_qblocks, int* bh, int* qb_long,
+                      int* qb_short) {
+    const g::PairWork w = g::causal_pair(block_id, bh_count, n_qblocks);
+    *bh = w.bh;
+    *qb_long = w.qb_long;
+    *qb_short = w.qb_short;
+}
 void geom_work_of(int block_id, int bh_count, int n_qblocks, int causal, int* bh, int* qb) {
     const g::Work w = g::work_of(block_id, bh_count, n_qblocks, causal != 0);
     *bh = w.bh;

@@ -28,6 +28,7 @@ def geo():
     so.geom_work_of.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_work_of_xcd.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_split_range.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 2
+    so.geom_causal_pair.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 3
     return so
 
 
@@ -438,3 +439,46 @@ def test_split_ranges_partition_each_query_block(geo):
             assert sum(x[1] for x in got) == n_all
             lens = [x[1] for x in got]
             assert min(lens) >= 1 and max(lens) <= tps and max(lens) - min(lens) <= 1
+
+
+PAIR_SHAPES = [(1, 1), (1, 2), (1, 3), (16, 64), (64, 16), (3, 9), (7, 5), (1, 65), (40, 12)]
+
+
+def _pairs(geo, bhc, nqb):
+    bh, lo_, hi_ = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    out = []
+    for bid in range(bhc * ((nqb + 1) // 2)):
+        geo.geom_causal_pair(bid, bhc, nqb, ctypes.byref(bh), ctypes.byref(hi_), ctypes.byref(lo_))
+        out.append((bh.value, hi_.value, lo_.value))
+    return out
+
+
+def test_causal_pairs_cover_every_query_block_once(geo):
+    for bhc, nqb in PAIR_SHAPES:
+        seen = []
+        for h, hi, lo in _pairs(geo, bhc, nqb):
+            assert 0 <= h < bhc and hi == nqb - 1 - lo if lo >= 0 else hi == (nqb - 1) // 2
+            seen.append((h, hi))
+            if lo >= 0:
+                assert lo < hi
+                seen.append((h, lo))
+        assert sorted(seen) == [(h, q) for h in range(bhc) for q in range(nqb)], (bhc, nqb)
+
+
+def test_causal_pairs_are_equal_work(geo):
+    """A causal query block qb visits qb + 1 key blocks: every pair visits n_qblocks + 1 (the
+    middle block of an odd count, alone, about half)."""
+    for bhc, nqb in PAIR_SHAPES:
+        for h, hi, lo in _pairs(geo, bhc, nqb):
+            work = (hi + 1) + (lo + 1 if lo >= 0 else 0)
+            assert work == nqb + 1 or (lo < 0 and nqb % 2 == 1 and work == (nqb + 1) // 2)
+
+
+def test_causal_pairs_keep_heads_on_one_xcd(geo):
+    """The (head, pair) items follow work_of_xcd's non-causal order."""
+    bh, qb = ctypes.c_int(), ctypes.c_int()
+    for bhc, nqb in PAIR_SHAPES:
+        pairs = (nqb + 1) // 2
+        for bid, (h, hi, lo) in enumerate(_pairs(geo, bhc, nqb)):
+            geo.geom_work_of_xcd(bid, bhc, pairs, 0, ctypes.byref(bh), ctypes.byref(qb))
+            assert (h, nqb - 1 - hi) == (bh.value, qb.value)
