@@ -64,6 +64,12 @@ namespace g = fa::geom;
 #define FA_OPTIMISTIC 1
 #endif
 
+// Causal ping-pong grids of workgroups that each run a (long, short) pair of query blocks of
+// one head (fa::geom::causal_pair; not in split-KV passes).
+#ifndef FA_CAUSAL_PAIRS
+#define FA_CAUSAL_PAIRS 1
+#endif
+
 // Main-loop schedules: SIMPLE (flash_fwd_kernel: each wave runs QK, softmax and PV of a tile in
 // turn), KSPLIT (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles),
 // PINGPONG16 (flash_fwd_pingpong16: two groups of waves alternate between an MFMA-only phase and
@@ -414,9 +420,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int items = bh_count * n_qblocks;
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
-    const g::Work w = SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
-                                         n_qblocks, CAUSAL)
-                            : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    // One (head, query block) item: the whole single-item kernel.
+    auto run_item = [&](const g::Work w) {
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const f16* kh = k + head;
     const f16* vh = v + head;
@@ -494,6 +499,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         store_o<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n, lane,
                    m_run, l_run, oacc);
     }
+    };
+    // (A causal grid of (long, short) query-block pairs, as the ping-pong runs, measured 2-9 %
+    // slower for this schedule on most shapes: its two or more workgroups per CU already hide
+    // the dispatch gaps that the pairs remove.)
+    run_item(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                                n_qblocks, CAUSAL)
+                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
 }
 
 // Split-KV combine: for each row, LSE = log2-sum-exp2 of the splits' base-2 LSEs, and
@@ -714,10 +726,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
 // or 4 phases before its first read, and replaces a tile whose last read was in an earlier
 // phase. Diagonal and tail tiles are masked inside the steady phases; only the last tile, which
 // has no successor to prefetch, goes through general_tiles16 afterwards.
-// Causal ping-pong grids of workgroups that each run a (long, short) pair of query blocks.
-#ifndef FA_CAUSAL_PAIRS
-#define FA_CAUSAL_PAIRS 1
-#endif
 // Wave priorities (s_setprio) of the ping-pong's matrix phase and softmax phase.
 #ifndef FA_PP_PRIO
 #define FA_PP_PRIO 1

@@ -20,8 +20,6 @@ RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" /
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
 SIMPLE, KSPLIT, PINGPONG16 = 0, 3, 4
-# flash_fwd_kernel<Tile, CAUSAL, SPLIT>: the split-KV build ends its template arguments in Lb1E
-SPLIT_SUFFIX_RE = re.compile(r"ELb[01]ELb1EEEv")
 
 
 def _load():
@@ -48,10 +46,6 @@ def _min_occupancy(name: str) -> int:
     if family == "flash_fwd_ksplit":
         return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
     assert family == "flash_fwd_kernel" and sched == SIMPLE, name
-    if SPLIT_SUFFIX_RE.search(name) and d == 64:
-        # the split-KV partial pass of causal d=64 (4-wave tile): its extra range bookkeeping
-        # takes it to 148 VGPRs, three waves per SIMD, measured as fast as the four-wave build
-        return 3
     return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
 
 
