@@ -8,7 +8,9 @@ One step = one non-causal forward followed by one causal forward on the same res
 value = algorithmic TFLOPS of the step, 4*B*H*N^2*d per non-causal pass plus half that per
 causal pass (bench/benchmark.py:142 of the reference), divided by the measured step time.
 
-Timing: W untimed warmup steps, then exactly K steps between two synchronizations; every
+Timing: untimed steps for at least --ramp-ms (300 ms; the clock settles from idle over a few
+hundred milliseconds under this load, longer than a short warmup), then W untimed warmup steps,
+then exactly K steps between two synchronizations; every
 launch is bracketed by HIP events recorded on the stream the kernel runs on (torch's current
 stream, which fa.forward launches on), so per-kernel averages come from the same run.
 roofline: the non-causal kernel (the larger share of the step) against the dense fp16 MFMA
@@ -118,6 +120,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     # The GPU takes tens of milliseconds to ramp its clock from idle: warm up past that.
     ap.add_argument("--warmup", type=int, default=20)
+    # ... and, before those W steps, untimed steps for at least this long (whatever W is): the
+    # clock takes a few hundred milliseconds to settle from idle under this load.
+    ap.add_argument("--ramp-ms", type=float, default=300.0)
     ap.add_argument("--config", default="cfg4")
     ap.add_argument("--variant", default="opt", choices=["baseline", "opt", "fp16acc"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -173,6 +178,13 @@ def main() -> int:
     for e in [t_start, t_stop] + [x for s_ev in ev for m_ev in s_ev for x in m_ev]:
         e.record()  # first use of each event outside the timed region
 
+    ramp_steps = 0
+    ramp0 = time.perf_counter()
+    while (time.perf_counter() - ramp0) * 1e3 < args.ramp_ms:
+        for _ in range(4):
+            out = step()
+        ramp_steps += 4
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         out = step()
     torch.cuda.synchronize()
@@ -241,6 +253,7 @@ def main() -> int:
         "roofline": roof(False) if False in modes else roof(True),
         "roofline_causal": roof(True) if True in modes and False in modes else None,
         "wall_s_timed": round(wall, 3),
+        "untimed_ramp": {"ms": round(args.ramp_ms, 1), "steps": ramp_steps},
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu:
