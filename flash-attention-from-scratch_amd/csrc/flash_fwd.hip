@@ -733,10 +733,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
 #ifndef FA_PP_SPRIO
 #define FA_PP_SPRIO 0
 #endif
-// Scheduler pattern: N times {R DS reads, V VALU instructions} (sched_group_barrier masks
-// 0x100 DS read, 0x002 VALU | 0x400 transcendental).
-template <int R, int V, int N>
+// Scheduler pattern: F DS reads, then N times {R DS reads, V VALU instructions}
+// (sched_group_barrier masks 0x100 DS read, 0x002 VALU | 0x400 transcendental).
+template <int R, int V, int N, int F = 0>
 __device__ __forceinline__ void sched_reads_valu() {
+    if constexpr (F > 0) __builtin_amdgcn_sched_group_barrier(0x100, F, 0);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
@@ -772,14 +773,26 @@ __device__ __forceinline__ void end_phase() {
 // fa::geom::pv16_key that the V^T operand reads. O^T in blocks oacc[db][qb] (features 16db..,
 // queries 16qb..). V tiles use the swizzle fa::geom::row_xor_m16; K tiles are stored so that
 // the K operand is read at the 32x32x16 path's conflict-free addresses (m16_kslot_row).
-// Fragment reads and softmax VALU of the softmax phase: N times {R reads, V VALU}; R must
-// divide the 24 reads.
-#ifndef FA_PP16_READS_PER
-#define FA_PP16_READS_PER 8
+// Fragment reads and softmax VALU of the softmax phase, as "F, R, V": F of the 24 reads first,
+// then groups of {R reads, V VALU instructions} (R divides 24 - F). Non-causal d=128 issues 16
+// reads (the K fragments and half of the V^T ones) before its first exponential, then 8 per 24
+// VALU: +0.7-1.0 % over {8 reads, 16 VALU} on three non-causal shapes, interleaved A/B; the
+// causal kernel measured 0 to -0.3 % with it and keeps {8, 16}.
+#ifndef FA_PP16_SCHED_NC128
+#define FA_PP16_SCHED_NC128 16, 8, 24
 #endif
-#ifndef FA_PP16_VALU_PER
-#define FA_PP16_VALU_PER 16
+#ifndef FA_PP16_SCHED
+#define FA_PP16_SCHED 0, 8, 16
 #endif
+template <int F_, int R_, int V_>
+struct ReadSched {
+    static constexpr int F = F_;
+    static constexpr int R = R_;
+    static constexpr int V = V_;
+};
+template <class T, bool CAUSAL>
+using PP16ReadSched = std::conditional_t<T::D == 128 && !CAUSAL, ReadSched<FA_PP16_SCHED_NC128>,
+                                         ReadSched<FA_PP16_SCHED>>;
 // Matrix phase: the refill goes after MFMA pair FA_PP16_MID; FA_PP16_PV_FIRST puts each pair's
 // P.V MFMA before its QK^T one.
 #ifndef FA_PP16_MID
@@ -1325,8 +1338,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             f16x8 p[G::QB][G::KS];
             bool overflow;
             softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
-            static_assert(G::READS % FA_PP16_READS_PER == 0, "FA_PP16_READS_PER must divide 24");
-            sched_reads_valu<FA_PP16_READS_PER, FA_PP16_VALU_PER, G::READS / FA_PP16_READS_PER>();
+            using RS = PP16ReadSched<T, CAUSAL>;
+            static_assert(RS::F <= G::READS && (G::READS - RS::F) % RS::R == 0,
+                          "the read groups must cover the 24 fragment reads");
+            sched_reads_valu<RS::R, RS::V, (G::READS - RS::F) / RS::R, RS::F>();
             end_phase<G == 1>();
             // matrix phase M_jj
             if (__builtin_expect(overflow, 0)) {
