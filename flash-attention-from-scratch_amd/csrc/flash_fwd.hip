@@ -777,7 +777,8 @@ __device__ __forceinline__ void end_phase() {
 // then groups of {R reads, V VALU instructions} (R divides 24 - F). Non-causal d=128 issues 16
 // reads (the K fragments and half of the V^T ones) before its first exponential, then 8 per 24
 // VALU: +0.7-1.0 % over {8 reads, 16 VALU} on three non-causal shapes, interleaved A/B; the
-// causal kernel measured 0 to -0.3 % with it and keeps {8, 16}.
+// causal kernel measured 0 to -0.3 % with it (and -0.2 to -1.0 % with seven other groupings)
+// and keeps {8, 16}.
 #ifndef FA_PP16_SCHED_NC128
 #define FA_PP16_SCHED_NC128 16, 8, 24
 #endif
