@@ -774,13 +774,13 @@ __device__ __forceinline__ void end_phase() {
 // queries 16qb..). V tiles use the swizzle fa::geom::row_xor_m16; K tiles are stored so that
 // the K operand is read at the 32x32x16 path's conflict-free addresses (m16_kslot_row).
 // Fragment reads and softmax VALU of the softmax phase, as "F, R, V": F of the 24 reads first,
-// then groups of {R reads, V VALU instructions} (R divides 24 - F). Non-causal d=128 issues 16
-// reads (the K fragments and half of the V^T ones) before its first exponential, then 8 per 24
-// VALU: +0.7-1.0 % over {8 reads, 16 VALU} on three non-causal shapes, interleaved A/B; the
-// causal kernel measured 0 to -0.3 % with it (and -0.2 to -1.0 % with seven other groupings)
-// and keeps {8, 16}.
-#ifndef FA_PP16_SCHED_NC128
-#define FA_PP16_SCHED_NC128 16, 8, 24
+// then groups of {R reads, V VALU instructions} (R divides 24 - F). Non-causal tiles issue 16
+// reads (the K fragments and half of the V^T ones) before the first exponential, then 8 per 24
+// VALU: at d=128 +0.7-1.0 % over {8 reads, 16 VALU} on three non-causal shapes, interleaved
+// A/B, and +0.3-0.4 % on the d=64 split-KV pass; the causal kernel measured 0 to -0.3 % with it
+// (and -0.2 to -1.0 % with seven other groupings) and keeps {8, 16}.
+#ifndef FA_PP16_SCHED_NC
+#define FA_PP16_SCHED_NC 16, 8, 24
 #endif
 #ifndef FA_PP16_SCHED
 #define FA_PP16_SCHED 0, 8, 16
@@ -792,8 +792,8 @@ struct ReadSched {
     static constexpr int V = V_;
 };
 template <class T, bool CAUSAL>
-using PP16ReadSched = std::conditional_t<T::D == 128 && !CAUSAL, ReadSched<FA_PP16_SCHED_NC128>,
-                                         ReadSched<FA_PP16_SCHED>>;
+using PP16ReadSched =
+    std::conditional_t<!CAUSAL, ReadSched<FA_PP16_SCHED_NC>, ReadSched<FA_PP16_SCHED>>;
 // Matrix phase: the refill goes after MFMA pair FA_PP16_MID; FA_PP16_PV_FIRST puts each pair's
 // P.V MFMA before its QK^T one.
 #ifndef FA_PP16_MID
