@@ -774,11 +774,13 @@ __device__ __forceinline__ void end_phase() {
 // queries 16qb..). V tiles use the swizzle fa::geom::row_xor_m16; K tiles are stored so that
 // the K operand is read at the 32x32x16 path's conflict-free addresses (m16_kslot_row).
 // Fragment reads and softmax VALU of the softmax phase, as "F, R, V": F of the 24 reads first,
-// then groups of {R reads, V VALU instructions} (R divides 24 - F). Non-causal tiles issue 16
-// reads (the K fragments and half of the V^T ones) before the first exponential, then 8 per 24
-// VALU: at d=128 +0.7-1.0 % over {8 reads, 16 VALU} on three non-causal shapes, interleaved
-// A/B, and +0.3-0.4 % on the d=64 split-KV pass; the causal kernel measured 0 to -0.3 % with it
-// (and -0.2 to -1.0 % with seven other groupings) and keeps {8, 16}.
+// then groups of {R reads, V VALU instructions} (R divides 24 - F). Non-causal tiles ask for
+// 16 reads before the first exponential and 8 per 24 VALU after; the compiler then issues all
+// 24 reads (8 K, 16 V^T) ahead of the softmax arithmetic: at d=128 +0.7-1.0 % over {8 reads,
+// 16 VALU} on three non-causal shapes, interleaved A/B, and +0.3-0.4 % on the d=64 split-KV
+// pass. (Asking for all 24 reads in one group, with the VALU left unordered, measured -5 %.)
+// The causal kernel measured 0 to -0.3 % with it (and -0.2 to -1.0 % with seven other
+// groupings) and keeps {8, 16}.
 #ifndef FA_PP16_SCHED_NC
 #define FA_PP16_SCHED_NC 16, 8, 24
 #endif
