@@ -190,6 +190,19 @@ def test_fp64_rows_long_causal():
         _close(out[0, bh, rows], ref)
 
 
+@pytest.mark.parametrize("n, d, causal", [(262067, 64, True), (131001, 128, False)])
+def test_fp64_rows_very_long_sequences(n, d, causal):
+    """Sequences of 128-256k keys with a ragged tail: 32-bit in-head offsets up to N*d*2 =
+    32 MiB per head, the main kernels' largest grids of one head pair, rows checked in fp64
+    at the start, the middle, around tile edges and at the last row."""
+    q, k, v = _qkv(1, 2, n, d, seed=12)
+    out = _fa().forward(q, k, v, causal=causal).float().cpu()
+    rows = [0, 255, 256, n // 2, n - 257, n - 2, n - 1]
+    for bh in range(2):
+        ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, causal, bh, rows)).float()
+        _close(out[0, bh, rows], ref)
+
+
 def test_c_abi_direct_call_matches_binding():
     """The raw C entry point (include/fa_hip.h) on torch's stream gives the binding's bits."""
     from fa import native
