@@ -804,6 +804,16 @@ using PP16ReadSched =
 #ifndef FA_PP16_PV_FIRST
 #define FA_PP16_PV_FIRST 0
 #endif
+// Unchecked softmax (non-causal ping-pong): the matrix phase adds the row sums of P after MFMA
+// pairs FA_PP16_SUM_PAIR, +2, ... (pair 8 measured best of 1, 4, 8, 10, 12, 13; one v_dot2
+// after each pair from 6, 8 or 10 instead lost 1-3 %). FA_PP16_UNCHECKED 0 keeps the per-tile
+// checked softmax in every kernel.
+#ifndef FA_PP16_SUM_PAIR
+#define FA_PP16_SUM_PAIR 8
+#endif
+#ifndef FA_PP16_UNCHECKED
+#define FA_PP16_UNCHECKED 1
+#endif
 // Per-tile geometry of the 16x16x32 path: D = 128 with 32-key tiles or D = 64 with 64-key
 // tiles; either way 32 MFMAs of each kind per wave and tile and 24 fragment reads.
 template <class T>
@@ -927,12 +937,72 @@ __device__ __forceinline__ void mask16(f32x4 (&s)[M16<T>::KB][M16<T>::QB], int k
             }
 }
 
+// Row max (log2 units: max over keys of s*c) of S = K Q^T over the key tiles [0, n_tiles) of a
+// non-causal item: the second pass of the unchecked softmax starts from it, so that no p exceeds
+// 1. One K tile at a time through one LDS buffer (DMA, wait, barrier, reads, barrier); keys >= nk,
+// which the DMA range check fills with zeros, are masked. A rare path: simple rather than fast.
+template <class T>
+__device__ __forceinline__ void rowmax16(const f16* kh, int n_tiles, int nk, int nk_load, int qk,
+                                         int lane, char* kl, const TileDma<T, true>& dma_k,
+                                         const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
+                                         float scale_log2, float (&m)[M16<T>::QB]) {
+    using G = M16<T>;
+    // Fragment offsets of its own: shared with the main loop's (CSE), they stay live across the
+    // whole item and push the d=128 kernel past 256 VGPRs into scratch.
+    int lane_own = lane;
+    asm volatile("" : "+v"(lane_own));
+    const Frag16<T> fr(lane_own);
+    float x[G::QB] = {-INFINITY, -INFINITY};
+    for (int t = 0; t < n_tiles; ++t) {
+        load_tile<T>(kh, t * T::BC, nk_load, kl, dma_k);
+        wait_vmem();
+        __syncthreads();
+        f32x4 sc[G::KB][G::QB];
+        qk16<T>(kl, fr, qf, sc);
+        if ((t + 1) * T::BC > nk) mask16<T, false>(sc, t * T::BC, nk, qk, lane);
+#pragma unroll
+        for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+            for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x[qb] = fmaxf(x[qb], sc[kb][qb][r]);
+        __syncthreads();  // every wave's reads of kl, before the next tile's DMA
+    }
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) m[qb] = max_xor32(max_xor16(x[qb])) * scale_log2;
+}
+
 // P^T operand slot i of k step t of query block qb: score accumulator i % 4 of key block
 // 2t + i / 4 (fa::geom::pv16_key).
 template <class T>
 __device__ __forceinline__ f16x8 pack16(const float (&e)[M16<T>::KB][4], int t) {
     return pack8(e[2 * t][0], e[2 * t][1], e[2 * t][2], e[2 * t][3], e[2 * t + 1][0],
                  e[2 * t + 1][1], e[2 * t + 1][2], e[2 * t + 1][3]);
+}
+
+// Unchecked optimistic softmax of a steady tile: p = exp2(s*c - m) against the running max,
+// packed to fp16, with neither row sums nor an overflow test here. The matrix phase adds the row
+// sums of the packed P (matrix_phase16<T, true>), in the shadow of its MFMAs; an overflowing p
+// becomes an infinite fp16 value and so an infinite row sum, which the workgroup tests once per
+// item (flash_fwd_pingpong16 then recomputes the item from its true row max).
+template <class T>
+__device__ __forceinline__ void softmax16_unchecked(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
+                                                    float scale_log2,
+                                                    const float (&m_run)[M16<T>::QB],
+                                                    f16x8 (&p)[M16<T>::QB][M16<T>::KS]) {
+    using G = M16<T>;
+    float e[G::QB][G::KB][4];
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                e[qb][kb][r] = exp2_fast(fmaf(s[kb][qb][r], scale_log2, -m_run[qb]));
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+        for (int t = 0; t < G::KS; ++t) p[qb][t] = pack16<T>(e[qb], t);
 }
 
 // Optimistic softmax against the running max (as softmax_optimistic): P in fp16 and l += row
@@ -981,7 +1051,7 @@ __device__ __forceinline__ void softmax16_optimistic(const f32x4 (&s)[M16<T>::KB
 
 // Exact online softmax of one tile (as softmax_tile): the tile max of a query spans the four
 // lanes lane % 16 + 16*i that hold its keys.
-template <class T>
+template <class T, bool ADD_SUM = true>
 __device__ __forceinline__ void softmax16_tile(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
                                                float scale_log2, float (&m_run)[M16<T>::QB],
                                                float (&l_run)[M16<T>::QB],
@@ -1016,8 +1086,9 @@ __device__ __forceinline__ void softmax16_tile(const f32x4 (&s)[M16<T>::KB][M16<
 #pragma unroll
         for (int t = 0; t < G::KS; ++t) {
             p[qb][t] = pack16<T>(e, t);
-            sum = sum8_f16(p[qb][t], sum);
+            if constexpr (ADD_SUM) sum = sum8_f16(p[qb][t], sum);
         }
+        // without ADD_SUM the caller adds the row sums of p (matrix_phase16<T, true>)
         l_run[qb] = (rescale ? l_run[qb] * alpha[qb] : l_run[qb]) + sum;
     }
 }
@@ -1048,16 +1119,17 @@ __device__ __forceinline__ void pv16(const f16x8 (&vf)[M16<T>::KS][M16<T>::DB],
 // Matrix phase: S^T_{j+1} (16 MFMAs: KB*QB independent chains of DC, step i on chain i % (KB*QB))
 // alternating with O^T += V_j^T P_j^T (16 MFMAs, independent); `mid` (the refill) after pair
 // FA_PP16_MID (the second pair: measured best of pairs 0-3 and 7, by about 1 %).
-template <class T, class Mid>
+template <class T, bool SUMS, class Mid>
 __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16<T>::DC],
                                                const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
                                                const f16x8 (&vf)[M16<T>::KS][M16<T>::DB],
                                                const f16x8 (&p)[M16<T>::QB][M16<T>::KS],
                                                f32x4 (&s)[M16<T>::KB][M16<T>::QB],
                                                f32x4 (&oacc)[M16<T>::DB][M16<T>::QB],
-                                               Mid&& mid) {
+                                               float (&l_run)[M16<T>::QB], Mid&& mid) {
     using G = M16<T>;
     constexpr int NCH = G::KB * G::QB;  // QK chains
+    static_assert(FA_PP16_SUM_PAIR + 2 * (G::QB * G::KS - 1) < 16, "row sums past the last pair");
 #pragma unroll
     for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
@@ -1082,6 +1154,18 @@ __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16
         if (i == FA_PP16_MID) {
             mid();
             __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (SUMS) {
+            // row sum of the packed P of (qb, t), four dependent v_dot2, after pair
+            // FA_PP16_SUM_PAIR + 2 (qb KS + t)
+#pragma unroll
+            for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+                for (int t = 0; t < G::KS; ++t)
+                    if (i == FA_PP16_SUM_PAIR + 2 * (qb * G::KS + t)) {
+                        l_run[qb] = sum8_f16(p[qb][t], l_run[qb]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
         }
     }
 }
@@ -1216,6 +1300,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
     constexpr bool PAIRED = CAUSAL && !SPLIT && FA_CAUSAL_PAIRS;
+    // Non-causal items run the unchecked softmax (softmax16_unchecked) and are recomputed, from
+    // the row max over all their keys (rowmax16), only if some p overflowed fp16 (then a row sum
+    // is infinite). The causal kernel measured 4.7 % slower with it and keeps the per-tile
+    // checked softmax.
+    constexpr bool UNCHECKED = !CAUSAL && FA_PP16_UNCHECKED;
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1228,8 +1317,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int grp = wave >> 2;
     const int items = bh_count * n_qblocks;
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
-    // One (head, query block) item: the whole single-item kernel.
-    auto run_item = [&](const g::Work w) {
+    // One (head, query block) item: the whole single-item kernel. With UNCHECKED, a first pass
+    // (checked_pass false) runs the unchecked softmax and returns false, having stored nothing,
+    // when a row sum came out non-finite; the second pass (checked_pass true) first takes the row
+    // max over all keys (rowmax16), so that no p can overflow, and always stores.
+    auto run_item = [&](const g::Work w, const bool checked_pass) -> bool {
+    constexpr bool FAST = UNCHECKED;
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const int q0 = w.qb * T::BR;
     const int qw = q0 + wave * 32;  // first query of this wave (Q loads, O stores)
@@ -1239,7 +1332,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int n_all = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
     const g::KeyRange range = SPLIT ? g::split_range(n_all, tiles_per_split, split)
                                     : g::KeyRange{0, n_all};
-    if (SPLIT && range.count == 0) return;  // workgroup-uniform: no such range
+    if (SPLIT && range.count == 0) return true;  // workgroup-uniform: no such range
     const int j_begin = range.begin;
     const int key0 = j_begin * T::BC;
     const int nk = n - key0;
@@ -1276,12 +1369,21 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 
     const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
     const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
+    f16x8 qf[G::QB][G::DC];
+    float m_run[G::QB] = {-INFINITY, -INFINITY};
+    if constexpr (FAST) {
+        // the second pass: the running max starts at the row max over all the item's keys
+        if (checked_pass) {
+            load_q16<T>(q + head, qw, n, lane, negate_q, qf);
+            rowmax16<T>(kh, n_tiles, nk, nk_load, qk, lane, kbuf(I0{}), dma_k, qf, scale_log2,
+                        m_run);
+        }
+    }
     load_tile<T>(kh, 0, nk_load, kbuf(I0{}), dma_k);
     load_tile<T>(vh, 0, nk_load, vbuf(I0{}), dma);
     load_tile<T>(kh, T::BC, nk_load, kbuf(I1{}), dma_k);
     load_tile<T>(kh, 2 * T::BC, nk_load, kbuf(I2{}), dma_k);
     load_tile<T>(vh, T::BC, nk_load, vbuf(I1{}), dma);
-    f16x8 qf[G::QB][G::DC];
     load_q16<T>(q + head, qw, n, lane, negate_q, qf);
     const Frag16<T> fr(lane);
 
@@ -1290,7 +1392,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     for (int db = 0; db < G::DB; ++db)
 #pragma unroll
         for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = f32x4{};
-    float m_run[G::QB] = {-INFINITY, -INFINITY};
     float l_run[G::QB] = {0.0F, 0.0F};
 
     wait_vmem();
@@ -1320,8 +1421,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             refill(3, I0{}, 2, I2{});
             end_phase<false>();
         }
-        auto tile = [&](int jj, auto r) {
+        // kind: 0 the checked optimistic softmax (its own row sums, an overflowing tile redone
+        // exactly); with FAST, 1 exact (the item's first tile) and 2 unchecked, both with the row
+        // sums added in the matrix phase.
+        auto tile = [&](int jj, auto r, auto kind) {
             constexpr int R = decltype(r)::value;
+            constexpr bool EXACT = FAST && decltype(kind)::value == 1;
+            constexpr bool UNCHECKED_TILE = FAST && decltype(kind)::value == 2;
             using Rj = std::integral_constant<int, R>;
             using Rj1 = std::integral_constant<int, (R + 1) % 3>;
             using Rj2 = std::integral_constant<int, (R + 2) % 3>;
@@ -1339,8 +1445,17 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             load_k16<T>(kbuf(Rj1{}), fr, kf);
             load_v16<T>(vbuf(Rj{}), fr, vf);
             f16x8 p[G::QB][G::KS];
-            bool overflow;
-            softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
+            bool overflow = false;
+            if constexpr (EXACT) {
+                float alpha[G::QB];
+                bool rescale;
+                softmax16_tile<T, false>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+                if (rescale) rescale16<T>(oacc, alpha);
+            } else if constexpr (UNCHECKED_TILE) {
+                softmax16_unchecked<T>(s, scale_log2, m_run, p);
+            } else {
+                softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
+            }
             using RS = PP16ReadSched<T, CAUSAL>;
             static_assert(RS::F <= G::READS && (G::READS - RS::F) % RS::R == 0,
                           "the read groups must cover the 24 fragment reads");
@@ -1354,7 +1469,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 if (rescale) rescale16<T>(oacc, alpha);
             }
             __builtin_amdgcn_s_setprio(FA_PP_PRIO);
-            matrix_phase16<T>(kf, qf, vf, p, s, oacc, [&] {
+            matrix_phase16<T, (EXACT || UNCHECKED_TILE)>(kf, qf, vf, p, s, oacc, l_run, [&] {
                 if constexpr (G == 0) {
                     refill(jj + 3, Rj{}, jj + 2, Rj2{});
                 } else {
@@ -1364,14 +1479,35 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             __builtin_amdgcn_s_setprio(FA_PP_SPRIO);
             end_phase<G == 0>();
         };
+        using Checked = std::integral_constant<int, 0>;
+        using Exact = std::integral_constant<int, 1>;
+        using Unchecked = std::integral_constant<int, 2>;
         int jj = 0;
-        for (; jj + 3 <= n_busy; jj += 3) {
-            tile(jj, I0{});
-            tile(jj + 1, I1{});
-            tile(jj + 2, I2{});
+        if constexpr (FAST) {
+            // tile 0 on its own (exact), then tiles 1.. in buffers 1, 2, 0, ...
+            auto rest = [&](auto kind) {
+                for (; jj + 3 <= n_busy; jj += 3) {
+                    tile(jj, I1{}, kind);
+                    tile(jj + 1, I2{}, kind);
+                    tile(jj + 2, I0{}, kind);
+                }
+                if (jj < n_busy) tile(jj, I1{}, kind);
+                if (jj + 1 < n_busy) tile(jj + 1, I2{}, kind);
+            };
+            if (n_busy > 0) {
+                tile(0, I0{}, Exact{});
+                jj = 1;
+            }
+            rest(Unchecked{});
+        } else {
+            for (; jj + 3 <= n_busy; jj += 3) {
+                tile(jj, I0{}, Checked{});
+                tile(jj + 1, I1{}, Checked{});
+                tile(jj + 2, I2{}, Checked{});
+            }
+            if (jj < n_busy) tile(jj, I0{}, Checked{});
+            if (jj + 1 < n_busy) tile(jj + 1, I1{}, Checked{});
         }
-        if (jj < n_busy) tile(jj, I0{});
-        if (jj + 1 < n_busy) tile(jj + 1, I1{});
         // Causal steady tiles whose keys are all masked for this wave (diagonal block, or a wave
         // past the end of the sequence): the wave keeps only its two barriers per tile and its
         // share of the refill DMA, in the order of a busy tile.
@@ -1410,6 +1546,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     vb[2] = v_lds2;
     general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
                                dma, fr, qf, s, oacc, scale_log2, m_run, l_run);
+    if constexpr (FAST) {
+        // an overflowing p makes its row sum infinite (NaN inputs make it NaN): decided for the
+        // whole workgroup, whose waves then redo the item together
+        if (!checked_pass) {
+            const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
+            if (__syncthreads_or(bad)) return false;
+        }
+    }
     if constexpr (SPLIT) {
         const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
         store16_partial<T>(o_part + part * n * T::D, lse_part + part * n, qw, n, lane, m_run,
@@ -1418,21 +1562,30 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
                    m_run, l_run, oacc);
     }
+    return true;
+    };
+    // With UNCHECKED: a second pass of the same code, from the true row max, when some p
+    // overflowed fp16 (the barrier of the failed pass's final test has ended all its LDS reads).
+    // One instance of the item code serves both passes.
+    auto run = [&](const g::Work w) {
+        bool checked_pass = false;
+#pragma clang loop unroll(disable)
+        while (!run_item(w, checked_pass)) checked_pass = true;
     };
     if constexpr (PAIRED) {
         // Causal grids: each workgroup runs the pair of query blocks (long, short) =
         // (n_qblocks - 1 - p, p), so that every workgroup has the same number of tiles
         // (fa::geom::causal_pair).
         const g::PairWork pw = g::causal_pair(static_cast<int>(blockIdx.x), bh_count, n_qblocks);
-        run_item(g::Work{pw.bh, pw.qb_long});
+        run_item(g::Work{pw.bh, pw.qb_long}, false);
         if (pw.qb_short >= 0) {
             __syncthreads();  // the first item's last LDS reads, before the second item's DMA
-            run_item(g::Work{pw.bh, pw.qb_short});
+            run_item(g::Work{pw.bh, pw.qb_short}, false);
         }
     } else {
-        run_item(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
-                                    n_qblocks, CAUSAL)
-                       : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
+        run(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                               n_qblocks, CAUSAL)
+                  : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
     }
 }
 
