@@ -779,8 +779,10 @@ __device__ __forceinline__ void end_phase() {
 // 24 reads (8 K, 16 V^T) ahead of the softmax arithmetic: at d=128 +0.7-1.0 % over {8 reads,
 // 16 VALU} on three non-causal shapes, interleaved A/B, and +0.3-0.4 % on the d=64 split-KV
 // pass. (Asking for all 24 reads in one group, with the VALU left unordered, measured -5 %.)
-// The causal kernel measured 0 to -0.3 % with it (and -0.2 to -1.0 % with seven other
-// groupings) and keeps {8, 16}.
+// The causal kernel with the per-tile checked softmax (now only its split-KV pass) measured 0 to
+// -0.3 % with it (and -0.2 to -1.0 % with seven other groupings) and keeps {8, 16}; with the
+// unchecked softmax up to the band it takes the non-causal order in every tile (+3.1 % on cfg4
+// causal, against +2.1 % with {8, 16} in every tile).
 #ifndef FA_PP16_SCHED_NC
 #define FA_PP16_SCHED_NC 16, 8, 24
 #endif
@@ -793,9 +795,9 @@ struct ReadSched {
     static constexpr int R = R_;
     static constexpr int V = V_;
 };
-template <class T, bool CAUSAL>
+template <class T, bool CHECKED_CAUSAL>
 using PP16ReadSched =
-    std::conditional_t<!CAUSAL, ReadSched<FA_PP16_SCHED_NC>, ReadSched<FA_PP16_SCHED>>;
+    std::conditional_t<!CHECKED_CAUSAL, ReadSched<FA_PP16_SCHED_NC>, ReadSched<FA_PP16_SCHED>>;
 // Matrix phase: the refill goes after MFMA pair FA_PP16_MID; FA_PP16_PV_FIRST puts each pair's
 // P.V MFMA before its QK^T one.
 #ifndef FA_PP16_MID
@@ -984,7 +986,8 @@ __device__ __forceinline__ f16x8 pack16(const float (&e)[M16<T>::KB][4], int t) 
 // packed to fp16, with neither row sums nor an overflow test here. The matrix phase adds the row
 // sums of the packed P (matrix_phase16<T, true>), in the shadow of its MFMAs; an overflowing p
 // becomes an infinite fp16 value and so an infinite row sum, which the workgroup tests once per
-// item (flash_fwd_pingpong16 then recomputes the item from its true row max).
+// item (flash_fwd_pingpong16 then recomputes the item with no unchecked tile: from its true row
+// max, non-causal, or with the per-tile checked softmax, causal).
 template <class T>
 __device__ __forceinline__ void softmax16_unchecked(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
                                                     float scale_log2,
@@ -1300,11 +1303,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
     constexpr bool PAIRED = CAUSAL && !SPLIT && FA_CAUSAL_PAIRS;
-    // Non-causal items run the unchecked softmax (softmax16_unchecked) and are recomputed, from
-    // the row max over all their keys (rowmax16), only if some p overflowed fp16 (then a row sum
-    // is infinite). The causal kernel measured 4.7 % slower with it and keeps the per-tile
-    // checked softmax.
-    constexpr bool UNCHECKED = !CAUSAL && FA_PP16_UNCHECKED;
+    // Items run the unchecked softmax (softmax16_unchecked) on their steady tiles after the
+    // first, causal items only up to the diagonal band, whose tiles keep the per-tile checked
+    // softmax; an item is recomputed only if some p overflowed fp16 (then a row sum is
+    // infinite): non-causal from the row max over all its keys (rowmax16), causal with every
+    // steady tile checked. The causal split-KV pass keeps the checked softmax throughout (a
+    // split range can start right of a row's keys, and the first tile's max is then -inf).
+    constexpr bool UNCHECKED = FA_PP16_UNCHECKED && !(CAUSAL && SPLIT);
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1371,7 +1376,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
     f16x8 qf[G::QB][G::DC];
     float m_run[G::QB] = {-INFINITY, -INFINITY};
-    if constexpr (FAST) {
+    if constexpr (FAST && !CAUSAL) {
         // the second pass: the running max starts at the row max over all the item's keys
         if (checked_pass) {
             load_q16<T>(q + head, qw, n, lane, negate_q, qf);
@@ -1435,7 +1440,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             // the one tile that can reach past the sequence end is the last, which runs in
             // general_tiles16. (Left to the compiler, the non-causal test is turned into 32
             // unconditional compare/select VALU instructions per tile.)
-            if constexpr (CAUSAL) {
+            if constexpr (CAUSAL && !UNCHECKED_TILE) {
                 if (g::tile_needs_mask(nk, jj * T::BC, T::BC, qk, CAUSAL)) {
                     mask16<T, CAUSAL>(s, jj * T::BC, nk, qk, lane);
                 }
@@ -1456,7 +1461,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             } else {
                 softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
             }
-            using RS = PP16ReadSched<T, CAUSAL>;
+            using RS = PP16ReadSched<T, CAUSAL && !FAST>;
             static_assert(RS::F <= G::READS && (G::READS - RS::F) % RS::R == 0,
                           "the read groups must cover the 24 fragment reads");
             sched_reads_valu<RS::R, RS::V, (G::READS - RS::F) / RS::R, RS::F>();
@@ -1498,7 +1503,22 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 tile(0, I0{}, Exact{});
                 jj = 1;
             }
-            rest(Unchecked{});
+            if constexpr (CAUSAL) {
+                // unchecked up to the first tile that some row of the workgroup must mask
+                // (keys 0..q0 are visible to every row; none in the second pass), checked from
+                // there (the diagonal band); the run stops at a multiple of three tiles so that
+                // both loops keep the buffer rotation
+                const int n_free =
+                    checked_pass ? 0 : min(n_busy, max(0, min(q0 - key0 + 1, nk)) / T::BC);
+                for (; jj + 3 <= n_free; jj += 3) {
+                    tile(jj, I1{}, Unchecked{});
+                    tile(jj + 1, I2{}, Unchecked{});
+                    tile(jj + 2, I0{}, Unchecked{});
+                }
+                rest(Checked{});
+            } else {
+                rest(Unchecked{});
+            }
         } else {
             for (; jj + 3 <= n_busy; jj += 3) {
                 tile(jj, I0{}, Checked{});
@@ -1577,10 +1597,19 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         // (n_qblocks - 1 - p, p), so that every workgroup has the same number of tiles
         // (fa::geom::causal_pair).
         const g::PairWork pw = g::causal_pair(static_cast<int>(blockIdx.x), bh_count, n_qblocks);
-        run_item(g::Work{pw.bh, pw.qb_long}, false);
-        if (pw.qb_short >= 0) {
+        // one call site of the item code for both items and both passes
+        bool second = false;
+        bool checked_pass = false;
+#pragma clang loop unroll(disable)
+        for (;;) {
+            if (!run_item(g::Work{pw.bh, second ? pw.qb_short : pw.qb_long}, checked_pass)) {
+                checked_pass = true;
+                continue;
+            }
+            if (second || pw.qb_short < 0) break;
             __syncthreads();  // the first item's last LDS reads, before the second item's DMA
-            run_item(g::Work{pw.bh, pw.qb_short}, false);
+            second = true;
+            checked_pass = false;
         }
     } else {
         run(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,

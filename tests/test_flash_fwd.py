@@ -95,17 +95,21 @@ def test_row_max_jumps_mid_sequence(d, causal):
 
 
 @pytest.mark.parametrize("d", [64, 128])
-def test_non_causal_overflow_recompute(d):
-    """The non-causal ping-pong kernels take p = exp2(s*c - m) against the first key tile's
-    max without testing each tile, and see an fp16 overflow of p only as an infinite row sum
-    at the end of the item, which they then recompute from the row max over all keys. Here
-    the scores of every other head rise by ~40 log2 units after the first 64 keys (an
-    overflow in nearly every row of those heads), and the other heads stay ~N(0, 1): the
-    single launch (C entry point, no routing) and the split-KV launch must both match the
-    oracle in every head, and repeat bit for bit."""
+@pytest.mark.parametrize("causal", [False, True])
+def test_overflow_recompute(d, causal):
+    """The ping-pong kernels take p = exp2(s*c - m) against the first key tile's max without
+    testing each tile (causal: up to the diagonal band, which keeps the per-tile test), and
+    see an fp16 overflow of p only as an infinite row sum at the end of the item, which they
+    then recompute. Here the scores of every other head rise by ~40 log2 units after the
+    first 64 keys (an overflow in nearly every row of those heads), and the other heads stay
+    ~N(0, 1): the single launch (C entry point, no routing) and the split-KV launch must both
+    match the oracle in every head, and repeat bit for bit. (At d=128 the single launch of
+    these shapes runs the ping-pong kernel; at d=64 the split-KV launch does.)"""
     from fa import native
 
-    b, h, n = 2, 8, 1100
+    b, h, n = 4, 16, (2500 if causal else 1100)
+    if d == 128:
+        assert native.tile_config(d, causal, "opt", n, b, h)["waves"] == 8
     g = torch.Generator().manual_seed(21)
     q = torch.randn(b, h, n, d, generator=g)
     k = torch.randn(b, h, n, d, generator=g)
@@ -113,20 +117,21 @@ def test_non_causal_overflow_recompute(d):
     k[:, 0::2, 64:] *= 8.0
     v = torch.randn(b, h, n, d, generator=g)
     q, k, v = (t.half().cuda() for t in (q, k, v))
+    print(f"case overflow B={b} H={h} N={n} d={d} causal={causal}", flush=True)
     outs = []
     for _ in range(2):
         o = torch.empty_like(q)
         p = native.make_params(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, n,
-                               d, d ** -0.5, False, "opt")
+                               d, d ** -0.5, causal, "opt")
         rc, msg = native.flash_fwd(p, torch.cuda.current_stream().cuda_stream)
         assert rc == native.FA_OK, msg
         torch.cuda.synchronize()
         outs.append(o)
     assert torch.equal(outs[0], outs[1])
-    ref = orc.attention_fp32(q, k, v)
+    ref = orc.attention_fp32(q, k, v, causal=causal)
     assert torch.isfinite(outs[0]).all()
     _close(outs[0], ref)
-    o_split, _ = _fa().forward_splitkv(q, k, v, causal=False, num_splits=3)
+    o_split, _ = _fa().forward_splitkv(q, k, v, causal=causal, num_splits=3)
     assert torch.isfinite(o_split).all()
     _close(o_split, ref)
 
