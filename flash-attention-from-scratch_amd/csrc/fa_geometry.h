@@ -260,4 +260,83 @@ constexpr PairWork causal_pair(int block_id, int bh_count, int n_qblocks) {
     return PairWork{w.bh, hi, hi != lo ? lo : -1};
 }
 
+// Makespan estimate, in key blocks, of the causal ping-pong grid of single query blocks: bh_count
+// copies of the lengths n_qblocks, ..., 1 (query block qb visits qb + 1 key blocks) dealt in
+// work_of's longest-first order to `slots` CUs, each taking the next workgroup when it frees (a
+// longest-first list schedule). Level by level: the bh_count blocks of one length give every CU
+// bh_count / slots of them and one more to each of the bh_count % slots least loaded CUs (the
+// list schedule can give two to one CU whose load trails by more than the length; the estimate
+// stays within one key block or 3 % of it from 9 query blocks up). Loads are kept as
+// ascending (load, count) groups, so a level costs O(groups). Returns -1 past kMaxGroups
+// groups. Host-side.
+constexpr int kMaxGroups = 256;
+inline long long causal_singles_makespan(long long bh_count, int n_qblocks, int slots) {
+    long long load[kMaxGroups + 1];
+    long long cnt[kMaxGroups + 1];
+    long long up_l[kMaxGroups + 1];
+    long long up_c[kMaxGroups + 1];
+    long long out_l[2 * kMaxGroups + 2];
+    long long out_c[2 * kMaxGroups + 2];
+    int ng = 1;
+    load[0] = 0;
+    cnt[0] = slots;
+    for (int len = n_qblocks; len >= 1; --len) {
+        const long long full = bh_count / slots;
+        long long r = bh_count % slots;
+        for (int i = 0; i < ng; ++i) load[i] += full * len;
+        // the r least loaded machines take one more block of this length
+        int nu = 0;
+        int i = 0;
+        while (r > 0) {
+            const long long take = cnt[i] < r ? cnt[i] : r;
+            up_l[nu] = load[i] + len;
+            up_c[nu] = take;
+            ++nu;
+            r -= take;
+            cnt[i] -= take;
+            if (cnt[i] == 0) ++i;
+        }
+        // merge the raised groups (ascending) with the rest (ascending, from group i)
+        int no = 0;
+        int a = 0;
+        int b = i;
+        while (a < nu || b < ng) {
+            const bool from_up = b >= ng || (a < nu && up_l[a] <= load[b]);
+            const long long l = from_up ? up_l[a] : load[b];
+            const long long c = from_up ? up_c[a++] : cnt[b++];
+            if (c == 0) continue;
+            if (no > 0 && out_l[no - 1] == l) {
+                out_c[no - 1] += c;
+            } else {
+                out_l[no] = l;
+                out_c[no] = c;
+                ++no;
+            }
+        }
+        if (no > kMaxGroups) return -1;
+        for (int k = 0; k < no; ++k) {
+            load[k] = out_l[k];
+            cnt[k] = out_c[k];
+        }
+        ng = no;
+    }
+    return load[ng - 1];
+}
+
+// Whether a causal ping-pong grid runs (long, short) pairs (causal_pair) or one query block per
+// workgroup in work_of's longest-first order. The ping-pong holds one workgroup per CU, so W
+// equal pair workgroups run in ceil(W / slots) rounds of n_qblocks + 1 key blocks each
+// (slots = CUs), while the single blocks end at causal_singles_makespan plus about 3 % on MI355X
+// (dispatch gaps between unequal workgroups: pairs measured 1.4-2.3 % faster where the two
+// schedules end together). Pairs are kept unless their last round is empty enough for the
+// singles to end first: 1x16x12288 d=128 (384 pairs, 1.5 rounds) ran 9.4 % and 3x16x6144
+// 18.6 % faster as singles. Host-side (launch grid choice).
+constexpr int kCus = 256;  // MI355X compute units: 8 XCDs of 32
+inline bool causal_pairs_pay(long long bh_count, int n_qblocks, int slots) {
+    const long long w = bh_count * ((n_qblocks + 1) / 2);
+    const long long pairs = (w + slots - 1) / slots * (n_qblocks + 1);
+    const long long singles = causal_singles_makespan(bh_count, n_qblocks, slots);
+    return singles < 0 || 100 * pairs <= 103 * singles;
+}
+
 }  // namespace fa::geom

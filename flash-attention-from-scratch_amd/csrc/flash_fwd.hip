@@ -65,7 +65,8 @@ namespace g = fa::geom;
 #endif
 
 // Causal ping-pong grids of workgroups that each run a (long, short) pair of query blocks of
-// one head (fa::geom::causal_pair; not in split-KV passes).
+// one head (fa::geom::causal_pair; not in split-KV passes), where fa::geom::causal_pairs_pay
+// finds that they end no later than single query blocks; 0 runs single blocks always.
 #ifndef FA_CAUSAL_PAIRS
 #define FA_CAUSAL_PAIRS 1
 #endif
@@ -1290,7 +1291,7 @@ __device__ __forceinline__ void general_tiles16(
     }
 }
 
-template <class T, bool CAUSAL, bool SPLIT = false>
+template <class T, bool CAUSAL, bool SPLIT = false, bool PAIRS = false>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
@@ -1302,7 +1303,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     static_assert(T::NW == 8, "ping-pong pairs waves w and w+4 on each of the four SIMDs");
     static_assert(T::NBUF == 3, "ping-pong keeps three K and three V tiles in LDS");
     static_assert(T::DMA_ITERS == 1, "one DMA request per tile and wave (vmcnt(2) keeps a pair)");
-    constexpr bool PAIRED = CAUSAL && !SPLIT && FA_CAUSAL_PAIRS;
+    constexpr bool PAIRED = CAUSAL && !SPLIT && PAIRS;
     // Items run the unchecked softmax (softmax16_unchecked) on their steady tiles after the
     // first, causal items only up to the diagonal band, whose tiles keep the per-tile checked
     // softmax; an item is recomputed only if some p overflowed fp16 (then a row sum is
@@ -1564,8 +1565,18 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     vb[0] = v_lds0;
     vb[1] = v_lds1;
     vb[2] = v_lds2;
-    general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
-                               dma, fr, qf, s, oacc, scale_log2, m_run, l_run);
+    if constexpr (CAUSAL && !SPLIT && !PAIRED) {
+        // causal single blocks: fragment offsets of the last tile's own, which the compiler
+        // would otherwise hoist out of the item loop and keep in scratch
+        int lane_g = lane;
+        asm volatile("" : "+v"(lane_g));
+        const Frag16<T> fr_g(lane_g);
+        general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
+                                   dma, fr_g, qf, s, oacc, scale_log2, m_run, l_run);
+    } else {
+        general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
+                                   dma, fr, qf, s, oacc, scale_log2, m_run, l_run);
+    }
     if constexpr (FAST) {
         // an overflowing p makes its row sum infinite (NaN inputs make it NaN): decided for the
         // whole workgroup, whose waves then redo the item together
@@ -1592,11 +1603,18 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #pragma clang loop unroll(disable)
         while (!run_item(w, checked_pass)) checked_pass = true;
     };
-    if constexpr (PAIRED) {
-        // Causal grids: each workgroup runs the pair of query blocks (long, short) =
+    if constexpr (CAUSAL && !SPLIT) {
+        // Causal grids: with PAIRS each workgroup runs the pair of query blocks (long, short) =
         // (n_qblocks - 1 - p, p), so that every workgroup has the same number of tiles
-        // (fa::geom::causal_pair).
-        const g::PairWork pw = g::causal_pair(static_cast<int>(blockIdx.x), bh_count, n_qblocks);
+        // (fa::geom::causal_pair); otherwise one query block, longest first (fa::geom::work_of;
+        // the launcher picks by fa::geom::causal_pairs_pay).
+        g::PairWork pw{};
+        if constexpr (PAIRED) {
+            pw = g::causal_pair(static_cast<int>(blockIdx.x), bh_count, n_qblocks);
+        } else {
+            const g::Work w = g::work_of(static_cast<int>(blockIdx.x), bh_count, n_qblocks, true);
+            pw = g::PairWork{w.bh, w.qb, -1};
+        }
         // one call site of the item code for both items and both passes
         bool second = false;
         bool checked_pass = false;
@@ -1797,10 +1815,13 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
             fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
         }
     } else if constexpr (T::SCHED == PINGPONG16) {
-        if constexpr (CAUSAL && FA_CAUSAL_PAIRS) {
-            grid = dim3(static_cast<unsigned>(bh) * static_cast<unsigned>((n_qblocks + 1) / 2));
-        }
         fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL>);
+        if constexpr (CAUSAL && FA_CAUSAL_PAIRS) {
+            if (g::causal_pairs_pay(bh, n_qblocks, g::kCus)) {
+                grid = dim3(static_cast<unsigned>(bh) * static_cast<unsigned>((n_qblocks + 1) / 2));
+                fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL, false, true>);
+            }
+        }
     } else if constexpr (T::SCHED == KSPLIT) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
     } else {

@@ -53,6 +53,12 @@ void geom_work_of_xcd(int block_id, int bh_count, int n_qblocks, int causal, int
     *bh = w.bh;
     *qb = w.qb;
 }
+long long geom_causal_singles_makespan(long long bh_count, int n_qblocks, int slots) {
+    return g::causal_singles_makespan(bh_count, n_qblocks, slots);
+}
+int geom_causal_pairs_pay(long long bh_count, int n_qblocks, int slots) {
+    return g::causal_pairs_pay(bh_count, n_qblocks, slots) ? 1 : 0;
+}
 void geom_causal_pair(int block_id, int bh_count, int n_qblocks, int* bh, int* qb_long,
                       int* qb_short) {
     const g::PairWork w = g::causal_pair(block_id, bh_count, n_qblocks);

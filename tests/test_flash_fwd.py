@@ -245,6 +245,35 @@ def test_fp64_rows_very_long_sequences(n, d, causal):
         _close(out[0, bh, rows], ref)
 
 
+@pytest.mark.parametrize("b, h, n", [(1, 16, 8192), (1, 16, 12288)])
+def test_causal_pairs_and_single_blocks(b, h, n):
+    """The causal d=128 ping-pong launch runs (long, short) query-block pairs when their rounds
+    fill the CUs and single blocks longest first otherwise (fa::geom::causal_pairs_pay): 1x16x8192
+    takes pairs (256 of them, one round), 1x16x12288 single blocks (384 pairs would leave half
+    the second round idle). Both grids against fp64 rows of the first and last heads."""
+    import ctypes
+    from pathlib import Path
+
+    from fa import native
+
+    geo = ctypes.CDLL(str(Path(__file__).resolve().parent / "geometry" / "libfa_geom.so"))
+    geo.geom_causal_pairs_pay.argtypes = [ctypes.c_longlong, ctypes.c_int, ctypes.c_int]
+    assert geo.geom_causal_pairs_pay(b * h, -(-n // 256), 256) == (1 if n == 8192 else 0)
+    print(f"case causal grid B={b} H={h} N={n}", flush=True)
+    q, k, v = _qkv(b, h, n, 128, seed=13)
+    o = torch.empty_like(q)
+    p = native.make_params(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, n, 128,
+                           128 ** -0.5, True, "opt")
+    rc, msg = native.flash_fwd(p, torch.cuda.current_stream().cuda_stream)
+    assert rc == native.FA_OK, msg
+    torch.cuda.synchronize()
+    out = o.float().cpu()
+    rows = [0, 255, 256, n // 2, n - 257, n - 256, n - 1]
+    for bh in (0, h - 1):
+        ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, True, bh, rows)).float()
+        _close(out[0, bh, rows], ref)
+
+
 def test_c_abi_direct_call_matches_binding():
     """The raw C entry point (include/fa_hip.h) on torch's stream gives the binding's bits."""
     from fa import native

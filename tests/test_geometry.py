@@ -29,6 +29,9 @@ def geo():
     so.geom_work_of_xcd.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_split_range.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_causal_pair.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 3
+    so.geom_causal_pairs_pay.argtypes = [ctypes.c_longlong, ctypes.c_int, ctypes.c_int]
+    so.geom_causal_singles_makespan.argtypes = [ctypes.c_longlong, ctypes.c_int, ctypes.c_int]
+    so.geom_causal_singles_makespan.restype = ctypes.c_longlong
     return so
 
 
@@ -482,3 +485,63 @@ def test_causal_pairs_keep_heads_on_one_xcd(geo):
         for bid, (h, hi, lo) in enumerate(_pairs(geo, bhc, nqb)):
             geo.geom_work_of_xcd(bid, bhc, pairs, 0, ctypes.byref(bh), ctypes.byref(qb))
             assert (h, nqb - 1 - hi) == (bh.value, qb.value)
+
+
+# (B*H, query blocks of 256 rows): measured on MI355X, d=128 causal, pairs against singles
+PAIRS_WIN = [(16, 64), (64, 16), (128, 12), (16, 32)]   # cfg4, cfg2, 8x16x3000, 1x16x8192
+SINGLES_WIN = [(16, 48), (48, 24), (32, 24), (32, 40)]  # 1x16x12288, 3x16x6144, 2x16x6144, 1x32x10240
+
+
+def test_causal_pairs_choice_follows_the_measurements(geo):
+    for bhc, nqb in PAIRS_WIN:
+        assert geo.geom_causal_pairs_pay(bhc, nqb, 256) == 1, (bhc, nqb)
+    for bhc, nqb in SINGLES_WIN:
+        assert geo.geom_causal_pairs_pay(bhc, nqb, 256) == 0, (bhc, nqb)
+
+
+def test_causal_pairs_taken_whenever_rounds_are_full(geo):
+    """An even number of query blocks and a pair count that fills whole rounds: the pairs'
+    time is total / slots exactly, which no schedule beats."""
+    for nqb in range(2, 130, 2):
+        for rounds in (1, 2, 3, 7):
+            slots = 256
+            pairs = rounds * slots
+            if pairs % (nqb // 2):
+                continue
+            assert geo.geom_causal_pairs_pay(pairs // (nqb // 2), nqb, slots) == 1, (nqb, rounds)
+
+
+def _lpt(bhc, nqb, slots):
+    """Longest-first list schedule of the single query blocks, one heap entry per CU."""
+    import heapq
+
+    loads = [0] * slots
+    for qb in range(nqb - 1, -1, -1):
+        for _ in range(bhc):
+            heapq.heapreplace(loads, loads[0] + qb + 1)
+    return max(loads)
+
+
+def test_causal_singles_makespan_estimates_a_list_schedule(geo):
+    """Within one key block or 3 % of a one-item-at-a-time list schedule from 9 query blocks
+    up (the causal ping-pong's range), exact where every CU gets the same count of each
+    length."""
+    for bhc in (1, 3, 8, 12, 16, 24, 40, 48, 64, 200, 300, 1000):
+        for nqb in range(9, 80, 4):
+            est, ref = geo.geom_causal_singles_makespan(bhc, nqb, 256), _lpt(bhc, nqb, 256)
+            assert abs(est - ref) <= max(1, 0.03 * ref), (bhc, nqb, est, ref)
+    for nqb in (1, 2, 9, 33):
+        assert geo.geom_causal_singles_makespan(512, nqb, 256) == _lpt(512, nqb, 256)
+
+
+def test_causal_pairs_choice_against_a_list_schedule(geo):
+    """Pairs are given up only where the singles' list schedule ends at least 1 % before the
+    pairs' rounds, and kept wherever it ends less than 5 % before them."""
+    for bhc in (1, 3, 8, 16, 24, 40, 64, 100):
+        for nqb in (9, 12, 16, 24, 33, 48, 64):
+            pairs = -(-bhc * ((nqb + 1) // 2) // 256) * (nqb + 1)
+            singles = _lpt(bhc, nqb, 256)
+            if geo.geom_causal_pairs_pay(bhc, nqb, 256) == 0:
+                assert singles <= 0.99 * pairs, (bhc, nqb, pairs, singles)
+            elif singles < 0.95 * pairs:
+                pytest.fail(f"pairs kept at {(bhc, nqb)}: {pairs} vs {singles}")
