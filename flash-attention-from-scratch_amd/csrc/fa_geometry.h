@@ -334,6 +334,10 @@ inline long long causal_singles_makespan(long long bh_count, int n_qblocks, int 
 constexpr int kCus = 256;  // MI355X compute units: 8 XCDs of 32
 inline bool causal_pairs_pay(long long bh_count, int n_qblocks, int slots) {
     const long long w = bh_count * ((n_qblocks + 1) / 2);
+    // 64 rounds or more: a partly empty last round costs under 2 %; more than 1024 query
+    // blocks: pairs too (the estimate's cost grows with the block count), which also keeps
+    // every product below in range
+    if (w >= 64LL * slots || n_qblocks > 1024) return true;
     const long long pairs = (w + slots - 1) / slots * (n_qblocks + 1);
     const long long singles = causal_singles_makespan(bh_count, n_qblocks, slots);
     return singles < 0 || 100 * pairs <= 103 * singles;

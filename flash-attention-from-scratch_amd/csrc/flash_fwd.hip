@@ -1641,9 +1641,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 // (csrc/kernels/flash_fwd.cu:597-612). On MI355X the best tile also depends on the sequence
 // length and the grid size, so the "opt" / "fp16acc" rows are split by N at thresholds found by
 // the tile sweep (FA2-paper shapes, B*N = 16k tokens):
-//   * d = 64: the 8-wave simple schedule at every length (256-row workgroups, 64-key tiles, two
-//     workgroups per CU); with the optimistic softmax its VALU work per tile is low enough that
-//     the four waves per SIMD keep the matrix pipe busier than the ping-pong does;
+//   * d = 64: the 8-wave simple schedule (256-row workgroups, 64-key tiles, two workgroups per
+//     CU); from 4096 keys (causal: 8192) the 16x16x32 ping-pong with 64-key tiles, when its
+//     one workgroup per CU fills whole rounds (non-causal: the last round at least 95 % full;
+//     causal: where the launcher runs pairs, fa::geom::causal_pairs_pay). Measured against the
+//     simple tile: non-causal +1.7 / +2.8 / +3.4 % at 4096 / 8192 / 16384 keys (B*N = 64k
+//     tokens, H = 16), causal +1.8 / +4.4 % at 8192 / 16384; with partly empty last rounds
+//     -0.1 % (3x16x6144) to -5.1 % (3x16x6144 causal), and causal -3.0 % at 4096;
 //   * d = 128: the 16x16x32 ping-pong for long sequences; below a threshold the 4-wave simple
 //     tile, which has no pipeline prologue and epilogue per workgroup (and, when causal, fewer
 //     diagonal tiles);
@@ -1670,6 +1674,18 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #endif
 #ifndef FA_OPT_D64_CAUSAL
 #define FA_OPT_D64_CAUSAL 64, 8, true, SIMPLE
+#endif
+#ifndef FA_OPT_D64_LONG
+#define FA_OPT_D64_LONG 64, 8, true, PINGPONG16
+#endif
+#ifndef FA_OPT_D64_CAUSAL_LONG
+#define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG16
+#endif
+#ifndef FA_D64_LONG_MIN_N
+#define FA_D64_LONG_MIN_N 4096
+#endif
+#ifndef FA_D64_CAUSAL_LONG_MIN_N
+#define FA_D64_CAUSAL_LONG_MIN_N 8192
 #endif
 #ifndef FA_OPT_D128_SHORT
 #define FA_OPT_D128_SHORT 32, 4, true, SIMPLE
@@ -1702,7 +1718,8 @@ struct Entry {
 enum TileId : int {
     BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
     OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
-    OPT_D64, OPT_D64_C, OPT_D128_SHORT, OPT_D128, OPT_D128_C_SHORT, OPT_D128_C,
+    OPT_D64, OPT_D64_C, OPT_D64_LONG, OPT_D64_C_LONG, OPT_D128_SHORT, OPT_D128, OPT_D128_C_SHORT,
+    OPT_D128_C,
 };
 template <int ID> struct Row;
 template <> struct Row<BASE_D64> : Entry<Tile<64, FA_BASE_D64>, false> {};
@@ -1715,6 +1732,8 @@ template <> struct Row<OPT_D128_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, fal
 template <> struct Row<OPT_D128_C_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, true> {};
 template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
 template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
+template <> struct Row<OPT_D64_LONG> : Entry<Tile<64, FA_OPT_D64_LONG>, false> {};
+template <> struct Row<OPT_D64_C_LONG> : Entry<Tile<64, FA_OPT_D64_CAUSAL_LONG>, true> {};
 template <> struct Row<OPT_D128_SHORT> : Entry<Tile<128, FA_OPT_D128_SHORT>, false> {};
 template <> struct Row<OPT_D128> : Entry<Tile<128, FA_OPT_D128>, false> {};
 template <> struct Row<OPT_D128_C_SHORT> : Entry<Tile<128, FA_OPT_D128_CAUSAL_SHORT>, true> {};
@@ -1730,7 +1749,18 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
         if (head_dim == 64) return causal ? OPT_D64_C_SMALL : OPT_D64_SMALL;
         return causal ? OPT_D128_C_SMALL : OPT_D128_SMALL;
     }
-    if (head_dim == 64) return causal ? OPT_D64_C : OPT_D64;
+    if (head_dim == 64) {
+        const int64_t nqb = (static_cast<int64_t>(n) + 255) / 256;
+        if (causal) {
+            const bool pp = n >= FA_D64_CAUSAL_LONG_MIN_N &&
+                            g::causal_pairs_pay(bh, static_cast<int>(nqb), g::kCus);
+            return pp ? OPT_D64_C_LONG : OPT_D64_C;
+        }
+        const int64_t items = bh * nqb;
+        const int64_t rounds = (items + g::kCus - 1) / g::kCus;
+        const bool pp = n >= FA_D64_LONG_MIN_N && 100 * items >= 95 * rounds * g::kCus;
+        return pp ? OPT_D64_LONG : OPT_D64;
+    }
     if (!causal) return n <= FA_D128_SHORT_MAX_N ? OPT_D128_SHORT : OPT_D128;
     return n <= FA_D128_CAUSAL_SHORT_MAX_N ? OPT_D128_C_SHORT : OPT_D128_C;
 }
@@ -1749,6 +1779,8 @@ decltype(auto) with_row(TileId id, F&& f) {
         case OPT_D128_C_SMALL: return f(Row<OPT_D128_C_SMALL>{});
         case OPT_D64: return f(Row<OPT_D64>{});
         case OPT_D64_C: return f(Row<OPT_D64_C>{});
+        case OPT_D64_LONG: return f(Row<OPT_D64_LONG>{});
+        case OPT_D64_C_LONG: return f(Row<OPT_D64_C_LONG>{});
         case OPT_D128_SHORT: return f(Row<OPT_D128_SHORT>{});
         case OPT_D128: return f(Row<OPT_D128>{});
         case OPT_D128_C_SHORT: return f(Row<OPT_D128_C_SHORT>{});

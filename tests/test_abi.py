@@ -122,9 +122,18 @@ def test_tile_config_invariants():
 def test_tile_config_rows():
     """The opt rows by N for a large grid (16 x 32 heads), and the small-grid rows."""
     simple64x8, simple128x4 = (256, 64, 8, 32768), (128, 32, 4, 32768)
-    for n in (1, 2048, 4097, 8193, 16384):                             # d=64: one row
+    pingpong64 = (256, 64, 8, 49152)                                   # three K + three V tiles
+    for n in (1, 2048, 4095):                                          # d=64, short: simple
         assert _tile(64, False, "opt", n) == simple64x8
+    for n in (1, 2048, 4096, 8191):
         assert _tile(64, True, "opt", n) == simple64x8
+    # from 4096 keys (causal 8192) the ping-pong, where its rounds of one workgroup per CU are
+    # (nearly) full: 16 x 32 heads give 512 * ceil(N / 256) items, whole rounds of 256
+    for n in (4096, 4097, 8193, 16384):
+        assert _tile(64, False, "opt", n) == pingpong64
+    assert _tile(64, True, "opt", 16384) == pingpong64                  # 4096 pairs
+    assert _tile(64, False, "opt", 6144, 3, 16) == simple64x8          # 1152 items: 4.5 rounds
+    assert _tile(64, True, "opt", 12288, 1, 16) == simple64x8          # 384 pairs: 1.5 rounds
     assert _tile(128, False, "opt", 1024) == simple128x4
     assert _tile(128, False, "opt", 1025) == (256, 32, 8, 49152)       # ping-pong
     assert _tile(128, True, "opt", 2048) == simple128x4

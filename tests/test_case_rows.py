@@ -23,10 +23,11 @@ def _tile(b, h, n, d, causal, variant="opt"):
 
 
 # Every (head_dim, causal, tile) the opt table can pick: the key split for small grids, the
-# simple tile, and at d=128 the ping-pong.
+# simple tile, and the ping-pong (d=64: long sequences with full rounds).
 OPT_ROWS = {
     (64, False, rows.SMALL64), (64, True, rows.SMALL64),
     (64, False, rows.SIMPLE64X8), (64, True, rows.SIMPLE64X8),
+    (64, False, rows.PP64), (64, True, rows.PP64),
     (128, False, rows.SMALL128), (128, True, rows.SMALL128),
     (128, False, rows.SIMPLE128X4), (128, True, rows.SIMPLE128X4),
     (128, False, rows.PP128), (128, True, rows.PP128),

@@ -42,6 +42,7 @@ LSE_CASES = [
     (4, 16, 1000, 64, True), (4, 16, 1000, 128, False),   # simple 8 and 4 waves, large grid
     (1, 16, 5000, 64, True), (2, 16, 2500, 128, False),   # simple d=64 long / ping-pong d=128
     (1, 16, 4000, 128, True),                             # ping-pong causal
+    (1, 8, 8000, 64, False),                              # ping-pong d=64
 ]
 
 

@@ -42,6 +42,7 @@ def _check(b, h, n, d, causal, want, seed=11):
 
 
 PP128 = (256, 32, 8, 49152)      # ping-pong, d=128
+PP64 = (256, 64, 8, 49152)       # ping-pong, d=64 (long sequences, full rounds)
 SIMPLE64X8 = (256, 64, 8, 32768)
 SIMPLE128X4 = (128, 32, 4, 32768)
 SMALL64 = (64, 64, 4, 65536)     # key split: 64 rows, 2 x 2 waves, BC=64
@@ -56,7 +57,10 @@ ROWS = [
     (4, 16, 1000, 64, False, SIMPLE64X8),
     (1, 32, 2500, 64, False, SIMPLE64X8),
     (4, 16, 1000, 64, True, SIMPLE64X8),
-    (1, 8, 8500, 64, True, SIMPLE64X8),
+    (1, 8, 8500, 64, True, PP64),             # 136 pairs: one round
+    (1, 16, 12288, 64, True, SIMPLE64X8),     # 384 pairs would run 1.5 rounds
+    (1, 8, 8000, 64, False, PP64),            # 256 items: one full round
+    (3, 16, 6100, 64, False, SIMPLE64X8),     # 1152 items: 4.5 rounds
     (4, 16, 1000, 128, False, SIMPLE128X4),
     (2, 16, 2500, 128, False, PP128),
     (4, 16, 1000, 128, True, SIMPLE128X4),
@@ -75,6 +79,9 @@ SWITCHES = [
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
     (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, SIMPLE64X8),
+    # d=64 ping-pong from 4096 keys (causal 8192)
+    (1, 16, 4095, 64, False, SIMPLE64X8), (1, 16, 4096, 64, False, PP64),
+    (1, 16, 8191, 64, True, SIMPLE64X8), (1, 16, 8192, 64, True, PP64),
 ]
 
 
