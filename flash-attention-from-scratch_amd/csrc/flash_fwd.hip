@@ -1700,7 +1700,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG16
 #endif
 #ifndef FA_D128_SHORT_MAX_N
-#define FA_D128_SHORT_MAX_N 1024
+#define FA_D128_SHORT_MAX_N 768
 #endif
 #ifndef FA_D128_CAUSAL_SHORT_MAX_N
 #define FA_D128_CAUSAL_SHORT_MAX_N 2048

@@ -134,8 +134,8 @@ def test_tile_config_rows():
     assert _tile(64, True, "opt", 16384) == pingpong64                  # 4096 pairs
     assert _tile(64, False, "opt", 6144, 3, 16) == simple64x8          # 1152 items: 4.5 rounds
     assert _tile(64, True, "opt", 12288, 1, 16) == simple64x8          # 384 pairs: 1.5 rounds
-    assert _tile(128, False, "opt", 1024) == simple128x4
-    assert _tile(128, False, "opt", 1025) == (256, 32, 8, 49152)       # ping-pong
+    assert _tile(128, False, "opt", 768) == simple128x4
+    assert _tile(128, False, "opt", 769) == (256, 32, 8, 49152)        # ping-pong
     assert _tile(128, True, "opt", 2048) == simple128x4
     assert _tile(128, True, "opt", 2049) == (256, 32, 8, 49152)
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,

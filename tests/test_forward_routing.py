@@ -139,7 +139,7 @@ TAIL_SHAPES = [
     (4, 16, 1001, 64, False, "opt"), (4, 16, 999, 64, True, "opt"),        # simple 8 waves
     (1, 32, 2501, 64, False, "opt"),                                        # simple, d=64
     (1, 8, 8000, 64, False, "opt"), (1, 8, 8500, 64, True, "opt"),         # ping-pong d=64
-    (4, 16, 1003, 128, False, "opt"), (4, 16, 1003, 128, True, "opt"),     # simple 4 waves
+    (8, 16, 703, 128, False, "opt"), (4, 16, 1003, 128, True, "opt"),      # simple 4 waves
     (2, 16, 2501, 128, False, "opt"), (1, 16, 4001, 128, True, "opt"),     # ping-pong d=128
     (2, 3, 333, 64, True, "baseline"), (2, 3, 333, 128, False, "baseline"),
 ]

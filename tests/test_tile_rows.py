@@ -61,7 +61,7 @@ ROWS = [
     (1, 16, 12288, 64, True, SIMPLE64X8),     # 384 pairs would run 1.5 rounds
     (1, 8, 8000, 64, False, PP64),            # 256 items: one full round
     (3, 16, 6100, 64, False, SIMPLE64X8),     # 1152 items: 4.5 rounds
-    (4, 16, 1000, 128, False, SIMPLE128X4),
+    (8, 16, 700, 128, False, SIMPLE128X4),
     (2, 16, 2500, 128, False, PP128),
     (4, 16, 1000, 128, True, SIMPLE128X4),
     (1, 16, 4000, 128, True, PP128),
@@ -74,7 +74,7 @@ def test_row(b, h, n, d, causal, want):
 
 
 SWITCHES = [
-    (2, 32, 1024, 128, False, SIMPLE128X4), (2, 32, 1025, 128, False, PP128),
+    (4, 32, 768, 128, False, SIMPLE128X4), (4, 32, 769, 128, False, PP128),
     (1, 32, 2048, 128, True, SIMPLE128X4), (1, 32, 2049, 128, True, PP128),
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
