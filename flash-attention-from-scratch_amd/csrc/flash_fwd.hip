@@ -780,12 +780,18 @@ __device__ __forceinline__ void end_phase() {
 // 24 reads (8 K, 16 V^T) ahead of the softmax arithmetic: at d=128 +0.7-1.0 % over {8 reads,
 // 16 VALU} on three non-causal shapes, interleaved A/B, and +0.3-0.4 % on the d=64 split-KV
 // pass. (Asking for all 24 reads in one group, with the VALU left unordered, measured -5 %.)
+// With the unchecked softmax, 8 per 32 VALU after the first 16 measured +0.4 % more on cfg4
+// and cfg2 (+0.3-0.6 % on the split-KV passes; 40 or 48 VALU, or 20 reads first and 4 per 32,
+// the same; 16 then 4 per 16: -2 %).
 // The causal kernel with the per-tile checked softmax (now only its split-KV pass) measured 0 to
 // -0.3 % with it (and -0.2 to -1.0 % with seven other groupings) and keeps {8, 16}; with the
-// unchecked softmax up to the band it takes the non-causal order in every tile (+3.1 % on cfg4
-// causal, against +2.1 % with {8, 16} in every tile).
+// unchecked softmax up to the band it takes {16, 8, 24} in every tile (+3.1 % on cfg4 causal,
+// against +2.1 % with {8, 16} in every tile; {16, 8, 32}: -0.1 %).
 #ifndef FA_PP16_SCHED_NC
-#define FA_PP16_SCHED_NC 16, 8, 24
+#define FA_PP16_SCHED_NC 16, 8, 32
+#endif
+#ifndef FA_PP16_SCHED_CU
+#define FA_PP16_SCHED_CU 16, 8, 24
 #endif
 #ifndef FA_PP16_SCHED
 #define FA_PP16_SCHED 0, 8, 16
@@ -796,9 +802,10 @@ struct ReadSched {
     static constexpr int R = R_;
     static constexpr int V = V_;
 };
-template <class T, bool CHECKED_CAUSAL>
-using PP16ReadSched =
-    std::conditional_t<!CHECKED_CAUSAL, ReadSched<FA_PP16_SCHED_NC>, ReadSched<FA_PP16_SCHED>>;
+template <class T, bool CAUSAL, bool CHECKED>
+using PP16ReadSched = std::conditional_t<
+    !CAUSAL, ReadSched<FA_PP16_SCHED_NC>,
+    std::conditional_t<CHECKED, ReadSched<FA_PP16_SCHED>, ReadSched<FA_PP16_SCHED_CU>>>;
 // Matrix phase: the refill goes after MFMA pair FA_PP16_MID; FA_PP16_PV_FIRST puts each pair's
 // P.V MFMA before its QK^T one.
 #ifndef FA_PP16_MID
@@ -1462,7 +1469,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             } else {
                 softmax16_optimistic<T>(s, scale_log2, m_run, l_run, overflow, p);
             }
-            using RS = PP16ReadSched<T, CAUSAL && !FAST>;
+            using RS = PP16ReadSched<T, CAUSAL, !FAST>;
             static_assert(RS::F <= G::READS && (G::READS - RS::F) % RS::R == 0,
                           "the read groups must cover the 24 fragment reads");
             sched_reads_valu<RS::R, RS::V, (G::READS - RS::F) / RS::R, RS::F>();
