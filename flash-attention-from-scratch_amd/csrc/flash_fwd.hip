@@ -1315,9 +1315,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     // first, causal items only up to the diagonal band, whose tiles keep the per-tile checked
     // softmax; an item is recomputed only if some p overflowed fp16 (then a row sum is
     // infinite): non-causal from the row max over all its keys (rowmax16), causal with every
-    // steady tile checked. The causal split-KV pass keeps the checked softmax throughout (a
-    // split range can start right of a row's keys, and the first tile's max is then -inf).
-    constexpr bool UNCHECKED = FA_PP16_UNCHECKED && !(CAUSAL && SPLIT);
+    // steady tile checked.
+    constexpr bool UNCHECKED = FA_PP16_UNCHECKED;
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1464,6 +1463,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 bool rescale;
                 softmax16_tile<T, false>(s, scale_log2, m_run, l_run, alpha, rescale, p);
                 if (rescale) rescale16<T>(oacc, alpha);
+                if constexpr (CAUSAL && SPLIT) {
+                    // a split range can start right of some rows' queries: such a row sees no
+                    // key in the range, and 0 keeps its later p at exp2(-inf) = 0 (and its
+                    // partial LSE at -inf, from l = 0)
+#pragma unroll
+                    for (int qb = 0; qb < G::QB; ++qb)
+                        m_run[qb] = m_run[qb] == -INFINITY ? 0.0F : m_run[qb];
+                }
             } else if constexpr (UNCHECKED_TILE) {
                 softmax16_unchecked<T>(s, scale_log2, m_run, p);
             } else {
@@ -1572,9 +1579,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     vb[0] = v_lds0;
     vb[1] = v_lds1;
     vb[2] = v_lds2;
-    if constexpr (CAUSAL && !SPLIT && !PAIRED) {
-        // causal single blocks: fragment offsets of the last tile's own, which the compiler
-        // would otherwise hoist out of the item loop and keep in scratch
+    if constexpr (CAUSAL && !PAIRED) {
+        // causal single blocks and split ranges: fragment offsets of the last tile's own, which
+        // the compiler would otherwise hoist out of the item loop and keep in scratch
         int lane_g = lane;
         asm volatile("" : "+v"(lane_g));
         const Frag16<T> fr_g(lane_g);
@@ -1594,7 +1601,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     }
     if constexpr (SPLIT) {
         const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
-        store16_partial<T>(o_part + part * n * T::D, lse_part + part * n, qw, n, lane, m_run,
+        // (causal: store offsets of the store's own, as for the last tile above)
+        int lane_s = lane;
+        int qw_s = qw;
+        if constexpr (CAUSAL) asm volatile("" : "+v"(lane_s), "+s"(qw_s));
+        store16_partial<T>(o_part + part * n * T::D, lse_part + part * n, qw_s, n, lane_s, m_run,
                            l_run, oacc);
     } else {
         store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
