@@ -783,10 +783,10 @@ __device__ __forceinline__ void end_phase() {
 // With the unchecked softmax, 8 per 32 VALU after the first 16 measured +0.4 % more on cfg4
 // and cfg2 (+0.3-0.6 % on the split-KV passes; 40 or 48 VALU, or 20 reads first and 4 per 32,
 // the same; 16 then 4 per 16: -2 %).
-// The causal kernel with the per-tile checked softmax (now only its split-KV pass) measured 0 to
-// -0.3 % with it (and -0.2 to -1.0 % with seven other groupings) and keeps {8, 16}; with the
-// unchecked softmax up to the band it takes {16, 8, 24} in every tile (+3.1 % on cfg4 causal,
-// against +2.1 % with {8, 16} in every tile; {16, 8, 32}: -0.1 %).
+// The causal kernel with the per-tile checked softmax in every tile (FA_PP16_UNCHECKED 0)
+// measured 0 to -0.3 % with it (and -0.2 to -1.0 % with seven other groupings) and keeps
+// {8, 16}; with the unchecked softmax up to the band it takes {16, 8, 24} in every tile (+3.1 %
+// on cfg4 causal, against +2.1 % with {8, 16} in every tile; {16, 8, 32}: -0.1 %).
 #ifndef FA_PP16_SCHED_NC
 #define FA_PP16_SCHED_NC 16, 8, 32
 #endif
