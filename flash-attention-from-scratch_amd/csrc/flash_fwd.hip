@@ -1982,14 +1982,18 @@ SplitPlan split_plan(const fa_params& p, int requested) {
 
 // Whether fa_flash_fwd leaves most of the GPU idle on these params and the automatic split-KV
 // plan is expected to be faster (measured on MI355X over few-head shapes at d = 64 and 128:
-// the split path wins from N = 4096 on grids of fewer 8-wave workgroups than CUs, except
-// causal d = 64, whose partial pass keeps the 4-wave simple tile and loses by a few percent).
+// the split path wins from N = 4096 on grids of fewer 8-wave workgroups than CUs; causal
+// d = 64, whose partial pass keeps the 4-wave simple tile, only from N = 16384: 1x1x16384
+// +48 %, 1x2x16384 +9 %, but 1x4x8192 -4 % and 1x8x4096 -20 %).
 #ifndef FA_SPLITKV_MIN_N
 #define FA_SPLITKV_MIN_N 4096
 #endif
+#ifndef FA_SPLITKV_MIN_N_D64_CAUSAL
+#define FA_SPLITKV_MIN_N_D64_CAUSAL 16384
+#endif
 bool splitkv_preferred(const fa_params& p) {
     if (p.variant == FA_VARIANT_BASELINE || p.seqlen < FA_SPLITKV_MIN_N) return false;
-    if (p.head_dim == 64 && p.causal) return false;
+    if (p.head_dim == 64 && p.causal && p.seqlen < FA_SPLITKV_MIN_N_D64_CAUSAL) return false;
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
     if (bh * ((static_cast<int64_t>(p.seqlen) + 255) / 256) >= FA_SMALL_GRID_WGS) return false;
     return split_plan(p, 0).n_splits >= 2;
