@@ -184,9 +184,18 @@ def build_all() -> None:
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--only", choices=sorted(TARGETS), action="append")
+    ap.add_argument("--define", action="append", default=[], metavar="NAME=VALUE",
+                    help="a kernel build option of libfa_hip.so (a macro of csrc/flash_fwd.hip), "
+                         "e.g. FA_PP16_UNCHECKED=0 for the per-tile checked softmax")
     args = ap.parse_args()
+    for d in args.define:
+        if not d.split("=", 1)[0].startswith("FA_"):
+            ap.error(f"--define takes the library's FA_* options, got {d}")
     for name in args.only or ALL:
-        TARGETS[name]()
+        if name == "lib":
+            build_lib([f"-D{d}" for d in args.define])
+        else:
+            TARGETS[name]()
 
 
 if __name__ == "__main__":
