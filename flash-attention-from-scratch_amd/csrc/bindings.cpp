@@ -5,7 +5,9 @@
 //
 // Grids too small to fill the GPU (few heads, long sequences): where the library's split-KV
 // plan says its split path is the faster one (fa_splitkv_info.preferred), `forward` and
-// `forward_lse` run it, with the workspace taken from torch's caching allocator;
+// `forward_lse` run it, and where fa_tail_plan plans a head split they run that (the first
+// heads in one launch, the rest split-KV), with the workspace taken from torch's caching
+// allocator;
 // fa_flash_fwd itself stays a single allocation-free launch.
 //
 // Same signature, defaults and error conditions as the reference binding
@@ -88,6 +90,37 @@ bool splitkv_if_preferred(const fa_params& p, float* lse, const torch::Tensor& q
     return true;
 }
 
+// Runs the head split of fa_tail_plan if it plans one (heads [0, h) in one launch, the rest
+// through split-KV, on the same stream); false (nothing launched) otherwise.
+bool tail_split_if_planned(const fa_params& p, float* lse, const torch::Tensor& q) {
+    int64_t h = 0;
+    if (fa_tail_plan(&p, &h) != FA_OK || h <= 0) return false;
+    const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
+    const int64_t head_elems = static_cast<int64_t>(p.seqlen) * p.head_dim;
+    auto advance = [&](const void* ptr) {
+        return static_cast<const void*>(static_cast<const at::Half*>(ptr) + h * head_elems);
+    };
+    fa_params first = p;
+    first.batch = 1;
+    first.heads = static_cast<int32_t>(h);
+    fa_params rest = p;
+    rest.batch = 1;
+    rest.heads = static_cast<int32_t>(bh - h);
+    rest.q = advance(p.q);
+    rest.k = advance(p.k);
+    rest.v = advance(p.v);
+    rest.o = const_cast<void*>(advance(p.o));
+    const hipStream_t s = stream_of(q);
+    check_rc(lse ? fa_flash_fwd_lse(&first, lse, s) : fa_flash_fwd(&first, s));
+    fa_splitkv_info info{};
+    check_rc(fa_splitkv_plan(&rest, 0, &info));
+    auto ws = torch::empty({static_cast<int64_t>(info.workspace_bytes / 4)},
+                           q.options().dtype(torch::kFloat));
+    check_rc(fa_flash_fwd_splitkv(&rest, lse ? lse + h * p.seqlen : nullptr, 0, ws.data_ptr(),
+                                  info.workspace_bytes, s));
+    return true;
+}
+
 torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
                       bool causal, std::optional<double> softmax_scale,
                       const std::string& variant) {
@@ -103,6 +136,7 @@ torch::Tensor forward(const torch::Tensor& q, const torch::Tensor& k, const torc
     // ("batch, heads and seqlen must be positive", "head_dim must be 64 or 128, got 0").
     if (q.size(2) == 0) return o;
     if (splitkv_if_preferred(p, nullptr, q)) return o;
+    if (tail_split_if_planned(p, nullptr, q)) return o;
     check_rc(fa_flash_fwd(&p, stream_of(q)));
     return o;
 }
@@ -122,6 +156,7 @@ std::tuple<torch::Tensor, torch::Tensor> forward_lse(const torch::Tensor& q,
     if (q.size(2) == 0) return {o, lse};
     // Same path choice as forward, so that O is bitwise forward's.
     if (splitkv_if_preferred(p, lse.data_ptr<float>(), q)) return {o, lse};
+    if (tail_split_if_planned(p, lse.data_ptr<float>(), q)) return {o, lse};
     check_rc(fa_flash_fwd_lse(&p, lse.data_ptr<float>(), stream_of(q)));
     return {o, lse};
 }

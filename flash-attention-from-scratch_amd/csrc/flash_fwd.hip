@@ -2010,6 +2010,32 @@ bool splitkv_preferred(const fa_params& p) {
     return split_plan(p, 0).n_splits >= 2;
 }
 
+// Non-causal head split for grids whose last round of ping-pong workgroups (one per CU) is
+// mostly empty: the first `heads` (b, h) heads run as one launch whose items fill whole rounds,
+// the rest through the split-KV pair, whose key ranges fill the CUs. Returns that head count, or
+// 0 to keep the single launch (causal grids choose pairs or single blocks instead). Measured on
+// MI355X, d = 128, through the binding against the single launch (one process, alternating):
+// 1x17x8192 (544 items: 2.1 rounds) +21.9 %, 1x36x4096 +14.7 %, 1x20x10000 +11.5 %,
+// 1x40x5000 +9.6 %.
+int64_t tail_heads(const fa_params& p) {
+    if (p.variant == FA_VARIANT_BASELINE || p.causal || p.seqlen < FA_SPLITKV_MIN_N) return 0;
+    const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
+    const TileId id = tile_id(p.head_dim, false, p.variant, p.seqlen, bh);
+    if (id != OPT_D128 && id != OPT_D64_LONG) return 0;  // the one-workgroup-per-CU rows
+    if (splitkv_preferred(p)) return 0;
+    const int64_t nqb = (static_cast<int64_t>(p.seqlen) + 255) / 256;
+    const int64_t items = bh * nqb;
+    const int64_t full = items / g::kCus;  // whole rounds
+    const int64_t last = items - full * g::kCus;
+    // two whole rounds at least (so that the first heads still fill the CUs), and a last round
+    // at most a third full (the split pass and its merge run the rest at a lower rate than the
+    // single launch: with the last round 3/8 full the split gained 2 %, with it half full it
+    // lost 4 %)
+    if (full < 2 || last == 0 || 3 * last > g::kCus) return 0;
+    const int64_t heads = full * g::kCus / nqb;
+    return heads > 0 && heads < bh ? heads : 0;
+}
+
 template <int D>
 int combine(const fa_params& p, const SplitPlan& sp, const float* o_part, const float* lse_part,
             float* lse, hipStream_t stream) {
@@ -2177,6 +2203,31 @@ int fa_flash_fwd_lse(const fa_params* params, float* lse, void* stream) {
         return fa::fail(FA_EINVAL, "flash_fwd_lse: lse must be a non-null, 4-byte aligned float*");
     }
     return run(*params, lse, stream);
+}
+
+int fa_tail_plan(const fa_params* params, int64_t* single_heads) {
+    fa::g_last_error.clear();
+    if (single_heads == nullptr) {
+        return fa::fail(FA_EINVAL, "fa_tail_plan: single_heads must not be NULL");
+    }
+    *single_heads = 0;
+    if (params == nullptr) return fa::fail(FA_EINVAL, "fa_tail_plan: params must not be NULL");
+    const fa_params& p = *params;
+    if (p.batch <= 0 || p.heads <= 0 || p.seqlen <= 0) {
+        return fa::fail(FA_EINVAL, "fa_tail_plan: batch, heads and seqlen must be positive");
+    }
+    if (p.head_dim != 64 && p.head_dim != 128) {
+        return fa::fail(FA_EINVAL, "fa_tail_plan: head_dim must be 64 or 128, got " +
+                                       std::to_string(p.head_dim));
+    }
+    if (static_cast<int64_t>(p.seqlen) * p.head_dim > INT32_MAX) {
+        return fa::fail(FA_EINVAL, "fa_tail_plan: seqlen * head_dim must be below 2^31");
+    }
+    if (p.variant > FA_VARIANT_FP16ACC) {
+        return fa::fail(FA_EINVAL, "fa_tail_plan: unknown variant " + std::to_string(p.variant));
+    }
+    *single_heads = fa::tail_heads(p);
+    return FA_OK;
 }
 
 int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info* out) {

@@ -72,6 +72,8 @@ def lib() -> ctypes.CDLL:
     so.fa_splitkv_plan.argtypes = [ctypes.POINTER(FaParams), ctypes.c_int32,
                                    ctypes.POINTER(FaSplitKvInfo)]
     so.fa_splitkv_plan.restype = ctypes.c_int
+    so.fa_tail_plan.argtypes = [ctypes.POINTER(FaParams), ctypes.POINTER(ctypes.c_int64)]
+    so.fa_tail_plan.restype = ctypes.c_int
     so.fa_flash_fwd_splitkv.argtypes = [ctypes.POINTER(FaParams), ctypes.c_void_p,
                                         ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint64,
                                         ctypes.c_void_p]
@@ -123,6 +125,16 @@ def splitkv_plan(params: FaParams, num_splits: int = 0) -> dict:
     if rc != FA_OK:
         raise ValueError(so.fa_last_error().decode())
     return {f: getattr(info, f) for f, _ in FaSplitKvInfo._fields_}
+
+
+def tail_plan(params: FaParams) -> int:
+    """fa_tail_plan: heads of the single launch in a head split (0: no split)."""
+    so = lib()
+    heads = ctypes.c_int64()
+    rc = so.fa_tail_plan(ctypes.byref(params), ctypes.byref(heads))
+    if rc != FA_OK:
+        raise ValueError(so.fa_last_error().decode())
+    return heads.value
 
 
 def flash_fwd_splitkv(params: FaParams, lse: int | None, num_splits: int, workspace: int,

@@ -99,12 +99,20 @@ typedef struct fa_splitkv_info {
     uint64_t workspace_bytes; /* num_splits * B * H * N * (D + 1) * 4                         */
     int32_t preferred;        /* 1 if the automatic split-KV plan is expected to beat
                                  fa_flash_fwd on these params (variant not baseline, a grid
-                                 that leaves most CUs idle, N >= 4096, not causal at D = 64),
-                                 else 0; independent of num_splits. The PyTorch binding's
-                                 forward takes the split path exactly when it is 1.           */
+                                 that leaves most CUs idle, N >= 4096; causal at D = 64:
+                                 N >= 16384), else 0; independent of num_splits. The PyTorch
+                                 binding's forward takes the split path exactly when it is 1. */
     int32_t reserved;         /* 0                                                            */
 } fa_splitkv_info;
 int fa_splitkv_plan(const fa_params* params, int32_t num_splits, fa_splitkv_info* out);
+
+/* Head split of a non-causal call whose grid of one-workgroup-per-CU items leaves its last round
+ * mostly empty (no counterpart in the reference): *single_heads = h > 0 means that the first h
+ * of the B*H heads (flattened [B*H, N, D]) are best run by fa_flash_fwd (batch 1, heads h: whole
+ * rounds of workgroups) and the other B*H - h by fa_flash_fwd_splitkv (pointers advanced by
+ * h*N*D elements, LSE by h*N); 0 means one fa_flash_fwd call. The PyTorch binding's forward and
+ * forward_lse follow it. Same argument checks as fa_splitkv_plan; host-only. */
+int fa_tail_plan(const fa_params* params, int64_t* single_heads);
 int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits,
                          void* workspace, uint64_t workspace_bytes, void* stream);
 

@@ -274,3 +274,48 @@ def test_splitkv_info_layout_matches_header(tmp_path):
                                           check=True).stdout.split()]
     S = native.FaSplitKvInfo
     assert got == [ctypes.sizeof(S), S.workspace_bytes.offset, S.preferred.offset]
+
+
+def _tail(b, h, n, d, causal=False, variant="opt"):
+    p = native.make_params(0x1000, 0x1000, 0x1000, 0x1000, b, h, n, d, d ** -0.5, causal, variant)
+    return native.tail_plan(p)
+
+
+def test_tail_plan_head_split():
+    """fa_tail_plan: non-causal ping-pong grids with two or more whole rounds of 256 items and a
+    last round at most half full keep the heads that fill the whole rounds in one launch."""
+    measured = {(1, 20, 10000): 19, (1, 40, 5000): 38, (1, 17, 8192): 16, (1, 36, 4096): 32}
+    for (b, h, n), want in measured.items():
+        assert _tail(b, h, n, 128) == want
+    for b, h, n in [(1, 20, 10000), (2, 12, 9000), (3, 16, 6144), (1, 40, 5000), (1, 17, 8192),
+                    (1, 36, 4096), (5, 7, 9999)]:
+        heads = _tail(b, h, n, 128)
+        nqb = -(-n // 256)
+        items = b * h * nqb
+        if heads:
+            assert 0 < heads < b * h
+            assert heads * nqb <= items // 256 * 256 < (heads + 1) * nqb
+            assert heads * nqb >= 512                 # the first launch keeps the ping-pong row
+            assert 3 * (items % 256) <= 256           # the last round was at most 1/3 full
+    # full rounds, causal, baseline, short, few-head (split-KV) and d=64 simple rows: no split
+    assert _tail(1, 16, 16384, 128) == 0
+    assert _tail(4, 16, 4096, 128) == 0
+    assert _tail(1, 20, 10000, 128, causal=True) == 0
+    assert _tail(1, 20, 10000, 128, variant="baseline") == 0
+    assert _tail(1, 45, 3000, 128) == 0
+    assert _tail(1, 2, 16384, 128) == 0
+    assert _tail(1, 20, 10000, 64) == 0
+    assert _tail(1, 45, 4096, 128) == 0               # last round 81 % full: one launch
+    assert _tail(3, 16, 6144, 128) == 0               # half full: the split measured slower
+    assert _tail(2, 12, 9000, 128) == 0               # 3/8 full: within noise, one launch
+
+
+def test_tail_plan_errors():
+    so = native.lib()
+    heads = ctypes.c_int64(7)
+    assert so.fa_tail_plan(None, ctypes.byref(heads)) == native.FA_EINVAL
+    p = native.make_params(0x1000, 0x1000, 0x1000, 0x1000, 1, 1, 64, 96, 1.0, False, "opt")
+    assert so.fa_tail_plan(ctypes.byref(p), ctypes.byref(heads)) == native.FA_EINVAL
+    assert b"head_dim" in so.fa_last_error() and heads.value == 0
+    p = native.make_params(0x1000, 0x1000, 0x1000, 0x1000, 1, 1, 64, 64, 1.0, False, "opt")
+    assert so.fa_tail_plan(ctypes.byref(p), None) == native.FA_EINVAL

@@ -117,6 +117,37 @@ def test_shapes_past_the_routing_boundaries_take_the_single_launch(b, h, n, d, c
     assert torch.equal(fa.forward(q, k, v, causal=causal), _single_launch(q, k, v, causal))
 
 
+@pytest.mark.parametrize("b,h,n,d", [(1, 17, 8192, 128), (1, 20, 10000, 128)])
+def test_head_split_of_a_mostly_empty_last_round(b, h, n, d):
+    """fa_tail_plan splits the heads: the first run as one single launch, the rest through
+    split-KV. forward must be bitwise those two calls on the two head ranges, forward_lse's O
+    bitwise forward's, and rows of the first, a boundary and the last head match fp64."""
+    import fa
+    from fa import native
+
+    p = native.make_params(0x1000, 0x1000, 0x1000, 0x1000, b, h, n, d, d ** -0.5, False, "opt")
+    heads = native.tail_plan(p)
+    print(f"case head split B={b} H={h} N={n} d={d} heads={heads}", flush=True)
+    assert 0 < heads < b * h
+    q, k, v = (t.cuda() for t in _qkv(b, h, n, d, seed=n + h))
+    out = fa.forward(q, k, v)
+    flat = [t.view(1, b * h, n, d) for t in (q, k, v)]
+    first = _single_launch(*(t[:, :heads] for t in flat), False)
+    rest, _ = fa.forward_splitkv(*(t[:, heads:] for t in flat))
+    assert torch.equal(out.view(1, b * h, n, d)[:, :heads], first)
+    assert torch.equal(out.view(1, b * h, n, d)[:, heads:], rest)
+    o_lse, lse = fa.forward_lse(q, k, v)
+    assert torch.equal(o_lse, out)
+    rows = [0, 255, 256, n // 2, n - 1]
+    outc = out.float().cpu().view(b * h, n, d)
+    for bh in (0, heads - 1, heads, b * h - 1):
+        ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, False, bh, rows)).float()
+        torch.testing.assert_close(outc[bh, rows], ref, atol=ATOL, rtol=RTOL)
+        lse_ref = torch.from_numpy(orc.lse_fp64_rows(q, k, False, bh, rows)).float()
+        torch.testing.assert_close(lse.view(b * h, n)[bh, rows].cpu(), lse_ref, atol=2e-3,
+                                   rtol=0)
+
+
 def test_baseline_variant_is_never_routed():
     import fa
 
