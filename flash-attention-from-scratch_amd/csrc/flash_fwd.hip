@@ -1456,7 +1456,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             // softmax phase S_jj. Only causal steady tiles can need a mask: without causality
             // the one tile that can reach past the sequence end is the last, which runs in
             // general_tiles16. (Left to the compiler, the non-causal test is turned into 32
-            // unconditional compare/select VALU instructions per tile.)
+            // unconditional compare/select VALU instructions per tile.) A causal item's
+            // unchecked tiles end before the first tile that any of its rows masks.
             if constexpr (CAUSAL && !UNCHECKED_TILE) {
                 if (g::tile_needs_mask(nk, jj * T::BC, T::BC, qk, CAUSAL)) {
                     mask16<T, CAUSAL>(s, jj * T::BC, nk, qk, lane);
