@@ -3,11 +3,11 @@
 # so only the kernel and a few copies are in the trace.
 #
 #   dev/counters.sh [name] [B H N D causal [variant]]     default: cfg4 1 16 16384 128 0 opt
-#   OUT=gpurun_out/counters/x dev/counters.sh cfg2c 4 16 4096 128 1
+#   OUT=out/counters/x dev/counters.sh cfg2c 4 16 4096 128 1
 #   FA_DEV_ARGS="--std 0.5 --boost-keys 0.01:8" dev/counters.sh cfg5 16 32 2048 64 1
 #       (FA_DEV_ARGS: extra fa_dev input options, e.g. the many-heads config's inputs)
 #
-# Writes OUT (default gpurun_out/counters/<name>): one rocprofv3 directory per pass and
+# Writes OUT (default out/counters/<name>): one rocprofv3 directory per pass and
 # summary.md, made by dev/counters.py. Passes (rocprofv3 collects each counter set in one run
 # of its own; a set stays within 8 SQ, 4 TCC and 2 GRBM counters):
 #   trace   kernel trace + per-kernel stats (durations)
@@ -31,7 +31,7 @@ if [[ ! -x $BIN ]]; then
     echo "build the driver first: python3 $here/../fa_build.py --only dev" >&2
     exit 2
 fi
-OUT=${OUT:-gpurun_out/counters/$NAME}
+OUT=${OUT:-out/counters/$NAME}
 mkdir -p "$OUT"
 export TMPDIR=${TMPDIR:-/tmp}
 # 1 checked launch, warmup launches for WARMUP_MS (default 100 ms: the clock ramps), 3 timed

@@ -167,7 +167,7 @@ def main(argv: list[str]) -> int:
     ap.add_argument("--bh", type=int, nargs=2, default=None, metavar=("B", "H"),
                     help="fixed batch and heads instead of the FA2-paper shapes")
     ap.add_argument("--impls", nargs="*", default=None, help="subset of implementations")
-    ap.add_argument("--csv", type=Path, default=Path("gpurun_out/sweep.csv"))
+    ap.add_argument("--csv", type=Path, default=Path("out/sweep.csv"))
     ap.add_argument("--md", type=Path, default=None, help="also write a markdown table")
     ap.add_argument("--budget-ms", type=float, default=1500.0, help="timing budget per cell")
     args = ap.parse_args(argv)
