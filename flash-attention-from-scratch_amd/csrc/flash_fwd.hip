@@ -2016,8 +2016,8 @@ bool splitkv_preferred(const fa_params& p) {
 // the rest through the split-KV pair, whose key ranges fill the CUs. Returns that head count, or
 // 0 to keep the single launch (causal grids choose pairs or single blocks instead). Measured on
 // MI355X, d = 128, through the binding against the single launch (one process, alternating):
-// 1x17x8192 (544 items: 2.1 rounds) +21.9 %, 1x36x4096 +14.7 %, 1x20x10000 +11.5 %,
-// 1x40x5000 +9.6 %.
+// 1x9x8192 (288 items: 1.1 rounds) +37.5 %, 1x17x4096 +34.9 %, 1x17x8192 (2.1 rounds) +21.9 %,
+// 1x36x4096 +14.7 %, 1x20x10000 +11.5 %, 1x40x5000 +9.6 %.
 int64_t tail_heads(const fa_params& p) {
     if (p.variant == FA_VARIANT_BASELINE || p.causal || p.seqlen < FA_SPLITKV_MIN_N) return 0;
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
@@ -2028,13 +2028,14 @@ int64_t tail_heads(const fa_params& p) {
     const int64_t items = bh * nqb;
     const int64_t full = items / g::kCus;  // whole rounds
     const int64_t last = items - full * g::kCus;
-    // two whole rounds at least (so that the first heads still fill the CUs), and a last round
-    // at most a third full (the split pass and its merge run the rest at a lower rate than the
-    // single launch: with the last round 3/8 full the split gained 2 %, with it half full it
-    // lost 4 %)
-    if (full < 2 || last == 0 || 3 * last > g::kCus) return 0;
+    // a last round at most a third full (the split pass and its merge run the rest at a lower
+    // rate than the single launch: with the last round 3/8 full the split gained 2 %, with it
+    // half full it lost 4 %)
+    if (full < 1 || last == 0 || 3 * last > g::kCus) return 0;
     const int64_t heads = full * g::kCus / nqb;
-    return heads > 0 && heads < bh ? heads : 0;
+    // the first heads must still fill the CUs (and keep this row of the tile table)
+    if (heads * nqb < FA_SMALL_GRID_WGS || heads >= bh) return 0;
+    return heads;
 }
 
 template <int D>
