@@ -2022,7 +2022,11 @@ int64_t tail_heads(const fa_params& p) {
     if (p.variant == FA_VARIANT_BASELINE || p.causal || p.seqlen < FA_SPLITKV_MIN_N) return 0;
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
     const TileId id = tile_id(p.head_dim, false, p.variant, p.seqlen, bh);
-    if (id != OPT_D128 && id != OPT_D64_LONG) return 0;  // the one-workgroup-per-CU rows
+    // the one-workgroup-per-CU rows, and the d = 64 simple row of long sequences, whose first
+    // heads then take the d = 64 ping-pong (whole rounds): d=64 1x9x8192 +36 %, 1x17x8192
+    // +24 %, 1x20x10000 +12 %, 1x36x4096 +10 %, 1x40x5000 +6 % against its single launch
+    const bool d64_long = id == OPT_D64 && p.seqlen >= FA_D64_LONG_MIN_N;
+    if (id != OPT_D128 && id != OPT_D64_LONG && !d64_long) return 0;
     if (splitkv_preferred(p)) return 0;
     const int64_t nqb = (static_cast<int64_t>(p.seqlen) + 255) / 256;
     const int64_t items = bh * nqb;

@@ -305,7 +305,8 @@ def test_tail_plan_head_split():
     assert _tail(1, 20, 10000, 128, variant="baseline") == 0
     assert _tail(1, 45, 3000, 128) == 0
     assert _tail(1, 2, 16384, 128) == 0
-    assert _tail(1, 20, 10000, 64) == 0
+    assert _tail(1, 20, 10000, 64) == 19              # d=64: the first heads take the ping-pong
+    assert _tail(1, 20, 3000, 64) == 0                # d=64 below 4096 keys: simple tile only
     assert _tail(1, 45, 4096, 128) == 0               # last round 81 % full: one launch
     assert _tail(3, 16, 6144, 128) == 0               # half full: the split measured slower
     assert _tail(2, 12, 9000, 128) == 0               # 3/8 full: within noise, one launch

@@ -117,7 +117,7 @@ def test_shapes_past_the_routing_boundaries_take_the_single_launch(b, h, n, d, c
     assert torch.equal(fa.forward(q, k, v, causal=causal), _single_launch(q, k, v, causal))
 
 
-@pytest.mark.parametrize("b,h,n,d", [(1, 17, 8192, 128), (1, 20, 10000, 128)])
+@pytest.mark.parametrize("b,h,n,d", [(1, 17, 8192, 128), (1, 20, 10000, 128), (1, 17, 8192, 64)])
 def test_head_split_of_a_mostly_empty_last_round(b, h, n, d):
     """fa_tail_plan splits the heads: the first run as one single launch, the rest through
     split-KV. forward must be bitwise those two calls on the two head ranges, forward_lse's O
