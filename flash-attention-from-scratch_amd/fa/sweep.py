@@ -102,6 +102,7 @@ def markdown_table(rows: list[dict], names: list[str]) -> str:
 
 
 def _impls():
+    import torch
     import torch.nn.functional as F
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
@@ -109,6 +110,20 @@ def _impls():
 
     def ours(variant):
         return lambda q, k, v, causal: fa.forward_variant(q, k, v, causal=causal, variant=variant)
+
+    def single(q, k, v, causal):
+        # one fa_flash_fwd launch through the C ABI, without the binding's split-KV routing
+        # and head split
+        from fa import native
+
+        o = torch.empty_like(q)
+        b, h, n, d = q.shape
+        p = native.make_params(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, h, n, d,
+                               d ** -0.5, causal, "opt")
+        rc, msg = native.flash_fwd(p, torch.cuda.current_stream().cuda_stream)
+        if rc != native.FA_OK:
+            raise RuntimeError(msg)
+        return o
 
     def sdpa(backend):
         def run(q, k, v, causal):
@@ -119,6 +134,7 @@ def _impls():
 
     return {
         "fa opt": ours("opt"),
+        "fa single": single,
         "fa splitkv": lambda q, k, v, causal: fa.forward_splitkv(q, k, v, causal=causal)[0],
         "fa fp16acc": ours("fp16acc"),
         "fa baseline": ours("baseline"),
@@ -166,6 +182,8 @@ def main(argv: list[str]) -> int:
     ap.add_argument("--hidden", type=int, default=2048, help="H * d")
     ap.add_argument("--bh", type=int, nargs=2, default=None, metavar=("B", "H"),
                     help="fixed batch and heads instead of the FA2-paper shapes")
+    ap.add_argument("--shapes", nargs="*", default=None, metavar="BxHxN",
+                    help="explicit shapes (with --d and --causal) instead of --n")
     ap.add_argument("--impls", nargs="*", default=None, help="subset of implementations")
     ap.add_argument("--csv", type=Path, default=Path("out/sweep.csv"))
     ap.add_argument("--md", type=Path, default=None, help="also write a markdown table")
@@ -180,8 +198,10 @@ def main(argv: list[str]) -> int:
     rows = []
     for d in args.d:
         for causal in map(bool, args.causal):
-            for n in args.n:
-                b, h = tuple(args.bh) if args.bh else paper_shape(n, d, args.tokens, args.hidden)
+            shapes = ([tuple(int(x) for x in s.split("x")) for s in args.shapes] if args.shapes
+                      else [(*(tuple(args.bh) if args.bh else
+                               paper_shape(n, d, args.tokens, args.hidden)), n) for n in args.n])
+            for b, h, n in shapes:
                 g = torch.Generator().manual_seed(0)
                 q, k, v = (torch.randn(b, h, n, d, generator=g).half().cuda() for _ in range(3))
                 ref, sl = reference_slice(q, k, v, causal)
