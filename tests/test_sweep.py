@@ -123,3 +123,25 @@ def test_sweep_runs_and_fa_rows_pass_the_gate(tmp_path):
         if r["impl"].startswith("fa "):
             assert r["status"] == "ok" and float(r["tflops"]) > 0, r
     assert "| 128 | 1 | 1024 | 16×16 |" in out_md.read_text()
+
+
+@pytest.mark.gpu
+def test_sweep_explicit_shapes_with_the_single_launch(tmp_path):
+    """--shapes runs the given BxHxN shapes; 'fa single' (the C-ABI launch without routing)
+    passes the same gate as fa.forward."""
+    if not torch.cuda.is_available():
+        pytest.skip("needs a ROCm GPU")
+    out_csv = tmp_path / "s.csv"
+    print("case sweep shapes 1x17x4096 2x3x700 d=128 non-causal", flush=True)
+    res = subprocess.run(
+        [sys.executable, "-m", "fa.sweep", "--shapes", "1x17x4096", "2x3x700", "--d", "128",
+         "--causal", "0", "--impls", "fa opt", "fa single", "--budget-ms", "100",
+         "--csv", str(out_csv)],
+        cwd=str(PKG), capture_output=True, text=True, timeout=240)
+    assert res.returncode == 0, res.stdout + res.stderr
+    with out_csv.open() as f:
+        rows = list(csv.DictReader(f))
+    assert sorted((int(r["B"]), int(r["H"]), int(r["N"]), r["impl"]) for r in rows) == [
+        (1, 17, 4096, "fa opt"), (1, 17, 4096, "fa single"),
+        (2, 3, 700, "fa opt"), (2, 3, 700, "fa single")]
+    assert all(r["status"] == "ok" and float(r["tflops"]) > 0 for r in rows), rows
