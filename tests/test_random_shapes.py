@@ -75,3 +75,55 @@ def test_random_case(i, b, h, n, d, causal, variant, scale):
         ref_lse = orc.lse_fp32(q[sl], k[sl], causal, scale)
         torch.testing.assert_close(lse[sl], ref_lse, atol=2e-3, rtol=0)
     assert math.isfinite(float(out.float().abs().max()))
+
+
+def _head_split_heads(bh, n):
+    """The head split rule restated (non-causal, N >= 4096, ping-pong grids of 256-row items
+    at one workgroup per CU): the heads whose items fill the whole rounds of 256, when the last
+    round is at most a third full and those heads still make 256 items or more; else 0."""
+    nqb = -(-n // 256)
+    items = bh * nqb
+    full, last = divmod(items, 256)
+    if full < 1 or last == 0 or 3 * last > 256:
+        return 0
+    heads = full * 256 // nqb
+    return heads if heads * nqb >= 256 and heads < bh else 0
+
+
+def _head_split_cases(count=6, seed=20261202):
+    rnd = random.Random(seed)
+    out = []
+    while len(out) < count:
+        d = rnd.choice([64, 128])
+        n = rnd.choice([4096, 4500, 5000, 6000, 8192, 9000, 10000])
+        bh = rnd.randint(2, max(2, (12 << 20) // (n * d)))
+        heads = _head_split_heads(bh, n)
+        if heads:
+            b = rnd.choice([x for x in (1, 2, 3) if bh % x == 0])
+            out.append((len(out), b, bh // b, n, d, heads))
+    return out
+
+
+@pytest.mark.parametrize("i,b,h,n,d,heads", _head_split_cases())
+def test_random_head_split_case(i, b, h, n, d, heads):
+    """Seeded shapes that take fa_tail_plan's head split: the library's plan equals the rule
+    restated above, and fa.forward / fa.forward_lse match the oracle on the first head, the
+    last head of the single launch, the first split head and the last head."""
+    import fa
+    from fa import native
+
+    p = native.make_params(0x1000, 0x1000, 0x1000, 0x1000, b, h, n, d, d ** -0.5, False, "opt")
+    print(f"case split {i}: B={b} H={h} N={n} d={d} heads={heads}", flush=True)
+    assert native.tail_plan(p) == heads
+    g = torch.Generator().manual_seed(2000 + i)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    out = fa.forward(qc, kc, vc).cpu()
+    _, lse = fa.forward_lse(qc, kc, vc)
+    lse = lse.cpu()
+    for f in sorted({0, heads - 1, heads, b * h - 1}):
+        bi, hi = divmod(f, h)
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl])
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+        torch.testing.assert_close(lse[sl], orc.lse_fp32(q[sl], k[sl], False), atol=2e-3, rtol=0)
