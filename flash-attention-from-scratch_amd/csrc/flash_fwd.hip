@@ -1936,11 +1936,25 @@ using SplitD64 = SplitRow<Tile<64, FA_SPLIT_D64>, false, FA_SPLIT_PLAN>;
 using SplitD64C = SplitRow<Tile<64, FA_SPLIT_D64_CAUSAL>, true, FA_SPLIT_PLAN_D64_CAUSAL>;
 using SplitD128 = SplitRow<Tile<128, FA_SPLIT_D128>, false, FA_SPLIT_PLAN>;
 using SplitD128C = SplitRow<Tile<128, FA_SPLIT_D128_CAUSAL>, true, FA_SPLIT_PLAN_D128_CAUSAL>;
+// Causal d = 128 on grids of fewer 256-row query blocks than CUs (the shapes fa.forward routes
+// to split-KV): the 4-wave simple tile, two or more workgroups per CU hiding each other's
+// prologue and epilogue, beats the ping-pong there (1x1x16384 +9.0 %, 1x4x8192 +11.1 %,
+// 1x2x16384 +2.1 %) and loses on larger grids (1x2x32768 -6.4 %).
+#ifndef FA_SPLIT_D128_CAUSAL_SMALL
+#define FA_SPLIT_D128_CAUSAL_SMALL 32, 4, true, SIMPLE
+#endif
+#ifndef FA_SPLIT_PLAN_D128_CAUSAL_SMALL
+#define FA_SPLIT_PLAN_D128_CAUSAL_SMALL 1024, 512
+#endif
+using SplitD128CSmall =
+    SplitRow<Tile<128, FA_SPLIT_D128_CAUSAL_SMALL>, true, FA_SPLIT_PLAN_D128_CAUSAL_SMALL>;
 
 template <class F>
-auto with_split_row(int head_dim, bool causal, F&& f) {
-    if (head_dim == 64) return causal ? f(SplitD64C{}) : f(SplitD64{});
-    return causal ? f(SplitD128C{}) : f(SplitD128{});
+auto with_split_row(const fa_params& p, F&& f) {
+    if (p.head_dim == 64) return p.causal ? f(SplitD64C{}) : f(SplitD64{});
+    if (!p.causal) return f(SplitD128{});
+    const int64_t blocks = static_cast<int64_t>(p.batch) * p.heads * ((p.seqlen + 255) / 256);
+    return blocks < FA_SMALL_GRID_WGS ? f(SplitD128CSmall{}) : f(SplitD128C{});
 }
 
 struct SplitPlan {
@@ -1960,7 +1974,7 @@ SplitPlan split_plan(const fa_params& p, int requested) {
     struct Consts {
         int br, bc, target_wgs, min_keys;
     };
-    const Consts rc = with_split_row(p.head_dim, p.causal != 0, [](auto row) {
+    const Consts rc = with_split_row(p, [](auto row) {
         using R = decltype(row);
         return Consts{R::T::BR, R::T::BC, R::TARGET_WGS, R::MIN_KEYS};
     });
@@ -2281,7 +2295,7 @@ static int splitkv_run(const fa_params& p, float* lse, const fa::SplitPlan& sp, 
                        void* stream) {
     const fa::Scale sc = fa::scale_of(p.softmax_scale);
     auto s = static_cast<hipStream_t>(stream);
-    return fa::with_split_row(p.head_dim, p.causal != 0, [&](auto row) {
+    return fa::with_split_row(p, [&](auto row) {
         return fa::splitkv<decltype(row)>(p, lse, sp, workspace, sc, s);
     });
 }

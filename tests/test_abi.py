@@ -189,15 +189,20 @@ def test_lse_entry_rejects_bad_lse_pointer():
 
 
 @pytest.mark.parametrize("b,h,n,d,causal", [(1, 2, 16384, 128, False), (1, 2, 16384, 128, True),
+                                            (1, 2, 32768, 128, True),
                                             (2, 8, 1000, 64, True), (1, 1, 1, 64, False),
                                             (16, 32, 2048, 64, True)])
 def test_splitkv_plan(b, h, n, d, causal):
     p = native.make_params(**{**GOOD, "batch": b, "heads": h, "seqlen": n, "head_dim": d,
                               "causal": causal})
     # Partial-pass rows: the 16x16x32 ping-pong (256 query rows; 32 keys per tile at d=128, 64 at
-    # d=64) except causal d=64 (simple tile, 128 rows, 64 keys); the automatic plan keeps at
-    # least 512 keys per range when not causal, 1024 causal d=128, 256 causal d=64.
-    bq, bc, min_keys = {(128, False): (256, 32, 512), (128, True): (256, 32, 1024),
+    # d=64) except causal d=64 (simple tile, 128 rows, 64 keys) and causal d=128 on grids of
+    # fewer 256-row blocks than CUs (simple 4-wave tile, 128 rows, 32 keys); the automatic plan
+    # keeps at least 512 keys per range when not causal, 1024 causal d=128 (512 on small
+    # grids), 256 causal d=64.
+    small = b * h * -(-n // 256) < 256
+    bq, bc, min_keys = {(128, False): (256, 32, 512),
+                        (128, True): (128, 32, 512) if small else (256, 32, 1024),
                         (64, False): (256, 64, 512), (64, True): (128, 64, 256)}[(d, causal)]
     max_tiles = -(-n // bc)
     for req in (0, 1, 2, 3, 7, 100000):
@@ -213,8 +218,11 @@ def test_splitkv_plan(b, h, n, d, causal):
     known = {
         # 2 heads x 64 query blocks x 512 key tiles / 256 target workgroups = 256 tiles
         (1, 2, 16384, 128, False): 256,
-        # causal: 2 heads x 8 x (1 + ... + 64) = 33280 (block, tile) pairs / 512 -> 65 tiles
+        # causal, small grid: 2 heads x 4 x (1 + ... + 128) = 66048 (block, tile) pairs / 1024
+        # target workgroups -> 65 tiles
         (1, 2, 16384, 128, True): 65,
+        # causal: 2 heads x 8 x (1 + ... + 128) = 132096 pairs / 512 -> 258 tiles
+        (1, 2, 32768, 128, True): 258,
     }
     if (b, h, n, d, causal) in known:
         assert native.splitkv_plan(p, 0)["tiles_per_split"] == known[(b, h, n, d, causal)]
