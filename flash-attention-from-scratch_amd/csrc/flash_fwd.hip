@@ -814,6 +814,12 @@ using PP16ReadSched = std::conditional_t<
 #ifndef FA_PP16_PV_FIRST
 #define FA_PP16_PV_FIRST 0
 #endif
+// The unchecked run tests for an overflow at the boundaries of chunks of 1, 2, 4, ... steps of
+// three tiles, at most FA_PP16_EXIT_STEPS steps long (outside its inner loop, which stays the
+// plain three-tile body).
+#ifndef FA_PP16_EXIT_STEPS
+#define FA_PP16_EXIT_STEPS 32
+#endif
 // Unchecked softmax (non-causal ping-pong): the matrix phase adds the row sums of P after MFMA
 // pairs FA_PP16_SUM_PAIR, +2, ... (pair 8 measured best of 1, 4, 8, 10, 12, 13; one v_dot2
 // after each pair from 6, 8 or 10 instead lost 1-3 %). FA_PP16_UNCHECKED 0 keeps the per-tile
@@ -824,16 +830,22 @@ using PP16ReadSched = std::conditional_t<
 #ifndef FA_PP16_UNCHECKED
 #define FA_PP16_UNCHECKED 1
 #endif
-// The first steady tile sets the reference max of the unchecked tiles FA_PP16_UNCHECKED_MARGIN
-// (exp2 units) above its own max, so that a later key overflows fp16 only when it exceeds the
-// first tile's max by 16 + MARGIN. With 8: cfg4 at inputs ~N(0, 1.6^2) (scores of standard
-// deviation 3.7 in exp2 units) ran at full speed instead of 27 % slower, at a cost of 0.3 %
-// on N(0, 1); from a standard deviation of about 6 many items still take the second pass.
-// The first tile's p are then at most 2^-8: keys more than 6 below its max are fp16
-// subnormals (the tests' fp64 rows hold at the north-star tolerance).
+// The first steady tile sets the reference max m of the unchecked tiles FA_PP16_UNCHECKED_MARGIN
+// (exp2 units) above its own max; a later key overflows fp16 when it exceeds the first tile's
+// max by 16 + MARGIN, and a key more than 25 - MARGIN below the first tile's max rounds to 0.
+// With MARGIN 0 (the default) m is a key's score, so m <= the row's true max: no p is flushed
+// unless it is below 2^-25 of the row's largest p, and the row sum is at least 1 (the key at m
+// gives p = 1), which bounds the weight of all flushed and subnormal p together by
+// N * 2^-25 of the row sum -- the guarantee of the reference's lazy softmax, whose stale max is
+// also a key's score (csrc/kernels/flash_fwd.cu:365-395). A positive MARGIN trades that for
+// fewer second passes on wide score spreads: with 8, a key that dominates the first tile (an
+// attention sink) pushed the other keys' p into the flush range, and at 16k keys rows lost
+// up to 2.7x the north-star tolerance with no second pass (tests/test_softmax_model.py).
 #ifndef FA_PP16_UNCHECKED_MARGIN
-#define FA_PP16_UNCHECKED_MARGIN 8
+#define FA_PP16_UNCHECKED_MARGIN 0
 #endif
+static_assert(FA_PP16_UNCHECKED_MARGIN >= 0 && FA_PP16_UNCHECKED_MARGIN <= 8,
+              "the lazy rescale (threshold 8) assumes the reference max is at most 8 above a key");
 // Per-tile geometry of the 16x16x32 path: D = 128 with 32-key tiles or D = 64 with 64-key
 // tiles; either way 32 MFMAs of each kind per wave and tile and 24 fragment reads.
 template <class T>
@@ -955,41 +967,6 @@ __device__ __forceinline__ void mask16(f32x4 (&s)[M16<T>::KB][M16<T>::QB], int k
                 const bool masked = key >= n || (CAUSAL && key > query);
                 s[kb][qb][r] = masked ? -INFINITY : s[kb][qb][r];
             }
-}
-
-// Row max (log2 units: max over keys of s*c) of S = K Q^T over the key tiles [0, n_tiles) of a
-// non-causal item: the second pass of the unchecked softmax starts from it, so that no p exceeds
-// 1. One K tile at a time through one LDS buffer (DMA, wait, barrier, reads, barrier); keys >= nk,
-// which the DMA range check fills with zeros, are masked. A rare path: simple rather than fast.
-template <class T>
-__device__ __forceinline__ void rowmax16(const f16* kh, int n_tiles, int nk, int nk_load, int qk,
-                                         int lane, char* kl, const TileDma<T, true>& dma_k,
-                                         const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
-                                         float scale_log2, float (&m)[M16<T>::QB]) {
-    using G = M16<T>;
-    // Fragment offsets of its own: shared with the main loop's (CSE), they stay live across the
-    // whole item and push the d=128 kernel past 256 VGPRs into scratch.
-    int lane_own = lane;
-    asm volatile("" : "+v"(lane_own));
-    const Frag16<T> fr(lane_own);
-    float x[G::QB] = {-INFINITY, -INFINITY};
-    for (int t = 0; t < n_tiles; ++t) {
-        load_tile<T>(kh, t * T::BC, nk_load, kl, dma_k);
-        wait_vmem();
-        __syncthreads();
-        f32x4 sc[G::KB][G::QB];
-        qk16<T>(kl, fr, qf, sc);
-        if ((t + 1) * T::BC > nk) mask16<T, false>(sc, t * T::BC, nk, qk, lane);
-#pragma unroll
-        for (int qb = 0; qb < G::QB; ++qb)
-#pragma unroll
-            for (int kb = 0; kb < G::KB; ++kb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) x[qb] = fmaxf(x[qb], sc[kb][qb][r]);
-        __syncthreads();  // every wave's reads of kl, before the next tile's DMA
-    }
-#pragma unroll
-    for (int qb = 0; qb < G::QB; ++qb) m[qb] = max_xor32(max_xor16(x[qb])) * scale_log2;
 }
 
 // P^T operand slot i of k step t of query block qb: score accumulator i % 4 of key block
@@ -1176,6 +1153,7 @@ __device__ __forceinline__ void matrix_phase16(const f16x8 (&kf)[M16<T>::KB][M16
             mid();
             __builtin_amdgcn_sched_barrier(0);
         }
+
         if constexpr (SUMS) {
             // row sum of the packed P of (qb, t), four dependent v_dot2, after pair
             // FA_PP16_SUM_PAIR + 2 (qb KS + t)
@@ -1323,10 +1301,17 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     constexpr bool PAIRED = CAUSAL && !SPLIT && PAIRS;
     // Items run the unchecked softmax (softmax16_unchecked) on their steady tiles after the
     // first, causal items only up to the diagonal band, whose tiles keep the per-tile checked
-    // softmax; an item is recomputed only if some p overflowed fp16 (then a row sum is
-    // infinite): non-causal from the row max over all its keys (rowmax16), causal with every
-    // steady tile checked.
+    // softmax; an item is recomputed, with every steady tile checked, only if some p overflowed
+    // fp16 (then a row sum is infinite). The workgroup sees an overflow in its unchecked run
+    // within two to three steps of three tiles and leaves the run early (pp_flags), so that an
+    // input on which most items overflow (outlier keys, wide score spreads) costs about one
+    // checked pass per item, not two passes.
     constexpr bool UNCHECKED = FA_PP16_UNCHECKED;
+    // Overflow flags of the unchecked run (0-1, one per chunk mod 2) and of the item's final
+    // test (2). Cleared at the start of an item's first pass; read with the lane and wave
+    // registers rather than threadIdx or __syncthreads_or, which would keep the work-item ids
+    // live across the item loop (past 256 VGPRs, into scratch).
+    __shared__ int pp_flags[3];
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1341,8 +1326,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
     // One (head, query block) item: the whole single-item kernel. With UNCHECKED, a first pass
     // (checked_pass false) runs the unchecked softmax and returns false, having stored nothing,
-    // when a row sum came out non-finite; the second pass (checked_pass true) first takes the row
-    // max over all keys (rowmax16), so that no p can overflow, and always stores.
+    // when a row sum came out non-finite; the second pass (checked_pass true) runs the checked
+    // softmax in every steady tile, which redoes an overflowing tile with a rescale, and always
+    // stores.
     auto run_item = [&](const g::Work w, const bool checked_pass) -> bool {
     constexpr bool FAST = UNCHECKED;
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
@@ -1393,13 +1379,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
     f16x8 qf[G::QB][G::DC];
     float m_run[G::QB] = {-INFINITY, -INFINITY};
-    if constexpr (FAST && !CAUSAL) {
-        // the second pass: the running max starts at the row max over all the item's keys
-        if (checked_pass) {
-            load_q16<T>(q + head, qw, n, lane, negate_q, qf);
-            rowmax16<T>(kh, n_tiles, nk, nk_load, qk, lane, kbuf(I0{}), dma_k, qf, scale_log2,
-                        m_run);
-        }
+    if constexpr (FAST) {
+        // cleared before the prologue's barrier; the previous pass or item read them before
+        // its own final barrier
+        if (!checked_pass && wave == 0 && lane < 3) static_cast<volatile int*>(pp_flags)[lane] = 0;
     }
     load_tile<T>(kh, 0, nk_load, kbuf(I0{}), dma_k);
     load_tile<T>(vh, 0, nk_load, vbuf(I0{}), dma);
@@ -1432,8 +1415,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = f32x4{};
     if (n_act > 0) qk16<T>(kbuf(I0{}), fr, qf, s);
 
-    auto steady = [&](auto group) {
+    // Returns true when the workgroup left its unchecked run on an overflow (FAST only).
+    auto steady = [&](auto group) -> bool {
         constexpr int G = decltype(group)::value;
+        bool aborted = false;
         auto refill = [&](int a, auto pa, int b, auto pb) {
             load_tile<T>(kh, a * T::BC, nk_load, kbuf(pa), dma_k);
             load_tile<T>(vh, b * T::BC, nk_load, vbuf(pb), dma);
@@ -1517,35 +1502,68 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         int jj = 0;
         if constexpr (FAST) {
             // tile 0 on its own (exact), then tiles 1.. in buffers 1, 2, 0, ...
-            auto rest = [&](auto kind) {
-                for (; jj + 3 <= n_busy; jj += 3) {
+            auto rest = [&](auto kind, int n_end) {
+                for (; jj + 3 <= n_end; jj += 3) {
                     tile(jj, I1{}, kind);
                     tile(jj + 1, I2{}, kind);
                     tile(jj + 2, I0{}, kind);
                 }
-                if (jj < n_busy) tile(jj, I1{}, kind);
-                if (jj + 1 < n_busy) tile(jj + 1, I2{}, kind);
+                if (jj < n_end) tile(jj, I1{}, kind);
+                if (jj + 1 < n_end) tile(jj + 1, I2{}, kind);
             };
             if (n_busy > 0) {
                 tile(0, I0{}, Exact{});
                 jj = 1;
             }
-            if constexpr (CAUSAL) {
-                // unchecked up to the first tile that some row of the workgroup must mask
-                // (keys 0..q0 are visible to every row; none in the second pass), checked from
-                // there (the diagonal band); the run stops at a multiple of three tiles so that
-                // both loops keep the buffer rotation
-                const int n_free =
-                    checked_pass ? 0 : min(n_busy, max(0, min(q0 - key0 + 1, nk)) / T::BC);
-                for (; jj + 3 <= n_free; jj += 3) {
+            // Unchecked tiles in steps of three, in chunks of 1, 2, 4, ... steps, at most
+            // FA_PP16_EXIT_STEPS (an overflow tends to come early, as the running max of the
+            // keys grows fastest at first). An overflowing p shows as an infinite row sum in the
+            // wave's l_run after the matrix phase of its tile. At chunk boundary c (the head of
+            // the chunk's first step) every
+            // wave first reads flag (c - 1) % 2 and leaves if it is set, then sets flag c % 2 if
+            // its own row sums are no longer finite. A flag is read one chunk (at least six
+            // barriers) after its writes, each of which has completed by its wave's next barrier
+            // (end_phase waits for its LDS writes), and written again one chunk after that read;
+            // so all waves read the same value and leave at the same boundary, i.e. after the
+            // same number of barriers (tests/test_abort_protocol.py). The workgroup leaves at
+            // most two chunks after the first overflow. The read waits at once (an LDS latency
+            // per chunk); the inner loop stays the plain three-tile body, whose timing is
+            // sensitive to any extra live value.
+            volatile int* flags = pp_flags;
+            // The exit needs every wave in the run. A causal wave that starts past the end of the
+            // sequence has no active tile and spends the run in the idle-tile loop below, never
+            // reading the flags, so a workgroup with such a wave (only a last query block) keeps
+            // to the full pass and its final test: no wave sets a flag there. (Non-causal waves
+            // all run every steady tile.)
+            const bool exit_ok = !CAUSAL || q0 + T::BR - 32 < n;
+            // Unchecked up to n_free, then checked: non-causal, the one to two tiles left over
+            // from the steps of three; causal, from the first tile that some row of the workgroup
+            // must mask (keys 0..q0 are visible to every row), i.e. the diagonal band. The
+            // second pass runs every steady tile checked.
+            const int n_free =
+                checked_pass ? 0
+                             : (CAUSAL ? min(n_busy, max(0, min(q0 - key0 + 1, nk)) / T::BC)
+                                       : n_busy);
+            int slot = 0;
+            int chunk = 1;  // steps
+            while (jj + 3 <= n_free) {
+                // (nothing can be set at the first boundary)
+                if (jj > 1 && __builtin_amdgcn_readfirstlane(flags[slot ^ 1]) != 0) {
+                    aborted = true;
+                    break;
+                }
+                const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
+                if (exit_ok && wave_any(bad) && lane == 0) flags[slot] = 1;
+                const int chunk_end = min(n_free, jj + 3 * chunk);
+                for (; jj + 3 <= chunk_end; jj += 3) {
                     tile(jj, I1{}, Unchecked{});
                     tile(jj + 1, I2{}, Unchecked{});
                     tile(jj + 2, I0{}, Unchecked{});
                 }
-                rest(Checked{});
-            } else {
-                rest(Unchecked{});
+                slot ^= 1;
+                chunk = min(2 * chunk, FA_PP16_EXIT_STEPS);
             }
+            rest(Checked{}, aborted ? jj : n_busy);
         } else {
             for (; jj + 3 <= n_busy; jj += 3) {
                 tile(jj, I0{}, Checked{});
@@ -1561,7 +1579,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         if constexpr (CAUSAL) {
             auto kb_at = [&](int b) { return b == 0 ? k_lds0 : (b == 1 ? k_lds1 : k_lds2); };
             auto vb_at = [&](int b) { return b == 0 ? v_lds0 : (b == 1 ? v_lds1 : v_lds2); };
-            for (int t = n_busy; t < n_steady; ++t) {
+            // (all waves leave an aborted run after the same tiles, so they skip the rest alike)
+            for (int t = aborted ? n_steady : n_busy; t < n_steady; ++t) {
                 const int r = t % 3;
                 end_phase<G == 1>();
                 if constexpr (G == 0) {
@@ -1575,12 +1594,15 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             }
         }
         if constexpr (G == 0) end_phase<false>();
+        return aborted;
     };
     if (n_steady > 0) {
-        if (grp == 0) {
-            steady(I0{});
-        } else {
-            steady(I1{});
+        const bool aborted = grp == 0 ? steady(I0{}) : steady(I1{});
+        if (aborted) {
+            // the DMA still in flight lands before the second pass refills the buffers
+            wait_vmem();
+            __syncthreads();
+            return false;
         }
     }
     char* kb[3];
@@ -1591,24 +1613,26 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     vb[0] = v_lds0;
     vb[1] = v_lds1;
     vb[2] = v_lds2;
-    if constexpr (CAUSAL) {
-        // causal: fragment offsets of the last tile's own, which the compiler would otherwise
-        // hoist out of the item loop and keep in scratch
+    {
+        // fragment offsets of the last tile's own, which the compiler would otherwise hoist out
+        // of the item loop and keep in scratch
         int lane_g = lane;
         asm volatile("" : "+v"(lane_g));
         const Frag16<T> fr_g(lane_g);
         general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
                                    dma, fr_g, qf, s, oacc, scale_log2, m_run, l_run);
-    } else {
-        general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
-                                   dma, fr, qf, s, oacc, scale_log2, m_run, l_run);
     }
     if constexpr (FAST) {
         // an overflowing p makes its row sum infinite (NaN inputs make it NaN): decided for the
-        // whole workgroup, whose waves then redo the item together
+        // whole workgroup (flag 2 after a barrier), whose waves then redo the item together.
+        // The flag is cleared again only by the next item, after the barrier between a pair's
+        // items.
         if (!checked_pass) {
+            volatile int* flags = pp_flags;
             const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
-            if (__syncthreads_or(bad)) return false;
+            if (wave_any(bad) && lane == 0) flags[2] = 1;
+            __syncthreads();
+            if (__builtin_amdgcn_readfirstlane(flags[2]) != 0) return false;
         }
     }
     if constexpr (SPLIT) {
@@ -1616,7 +1640,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         // (causal: store offsets of the store's own, as for the last tile above)
         int lane_s = lane;
         int qw_s = qw;
-        if constexpr (CAUSAL) asm volatile("" : "+v"(lane_s), "+s"(qw_s));
+        asm volatile("" : "+v"(lane_s), "+s"(qw_s));
         store16_partial<T>(o_part + part * n * T::D, lse_part + part * n, qw_s, n, lane_s, m_run,
                            l_run, oacc);
     } else {
@@ -1625,9 +1649,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     }
     return true;
     };
-    // With UNCHECKED: a second pass of the same code, from the true row max, when some p
-    // overflowed fp16 (the barrier of the failed pass's final test has ended all its LDS reads).
-    // One instance of the item code serves both passes.
+    // With UNCHECKED: a second pass of the same code, every steady tile checked, when some p
+    // overflowed fp16 (the final barrier of the failed pass has ended all its LDS reads). One
+    // instance of the item code serves both passes.
     auto run = [&](const g::Work w) {
         bool checked_pass = false;
 #pragma clang loop unroll(disable)
@@ -1645,19 +1669,23 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             const g::Work w = g::work_of(static_cast<int>(blockIdx.x), bh_count, n_qblocks, true);
             pw = g::PairWork{w.bh, w.qb, -1};
         }
-        // one call site of the item code for both items and both passes
+        // One call site of the item code for both items and both passes. The two items of a
+        // pair are query blocks of one head, the second seeing a prefix of the first's keys: if
+        // the first needed the checked pass, the second runs it at once.
         bool second = false;
         bool checked_pass = false;
+        bool redone = false;
 #pragma clang loop unroll(disable)
         for (;;) {
             if (!run_item(g::Work{pw.bh, second ? pw.qb_short : pw.qb_long}, checked_pass)) {
                 checked_pass = true;
+                redone = true;
                 continue;
             }
             if (second || pw.qb_short < 0) break;
             __syncthreads();  // the first item's last LDS reads, before the second item's DMA
             second = true;
-            checked_pass = false;
+            checked_pass = redone;
         }
     } else {
         run(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
@@ -2139,7 +2167,14 @@ extern "C" {
 
 const char* fa_last_error(void) { return fa::g_last_error.c_str(); }
 
-const char* fa_version(void) { return "fa_hip 0.1.0 gfx950"; }
+#define FA_STR_(x) #x
+#define FA_STR(x) FA_STR_(x)
+// The softmax build options follow the version, so that a caller (and the CPU tests' model of
+// the ping-pong arithmetic) can read how this library was compiled.
+const char* fa_version(void) {
+    return "fa_hip 0.2.0 gfx950 pp16_unchecked=" FA_STR(FA_PP16_UNCHECKED) " pp16_margin=" FA_STR(
+        FA_PP16_UNCHECKED_MARGIN);
+}
 
 int fa_tile_config(const fa_params* params, fa_tile_info* out) {
     fa::g_last_error.clear();

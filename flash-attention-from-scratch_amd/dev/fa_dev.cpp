@@ -1,13 +1,17 @@
 // fa_dev -- standalone driver of the attention forward, without Python or PyTorch.
 //
 //   fa_dev [B H N D causal iters variant] [--lib PATH] [--warmup-ms MS] [--seed S] [--json]
-//          [--std X] [--boost-keys FRAC:FACTOR] [--splitkv S]
+//          [--std X] [--boost-keys FRAC:FACTOR] [--sink NATS] [--splitkv S]
 //          defaults:  4 8 4096 128 0 20 opt,  --lib <this dir>/../fa/libfa_hip.so
 //   variant: base | baseline | opt | fp16acc
 //   --std X                 inputs ~ N(0, X^2) instead of N(0, 1)
 //   --boost-keys FRAC:FAC   multiply floor(FRAC * N) key rows of every head (a seeded random
 //                           choice) by FAC, as the benchmark's many-heads config does
 //                           (--std 0.5 --boost-keys 0.01:8): row maxima then jump mid-sequence
+//   --sink NATS             an attention sink: feature 0 of every query set to 4 and of key 0
+//                           of every head to NATS * sqrt(D) / 4, so that key 0 scores about
+//                           NATS above the other keys for every query (as tests/
+//                           test_softmax_model.py's sink_qkv)
 //   --splitkv S             run the split-KV entry point (fa_flash_fwd_splitkv) with S key
 //                           ranges per query block (0 = the library's automatic plan) and a
 //                           workspace of the plan's size; the timing covers both launches
@@ -155,6 +159,7 @@ struct Options {
     float std = 1.0F;
     double boost_frac = 0.0;
     float boost = 1.0F;
+    float sink = 0.0F;  // 0: no sink
     int splitkv = -1;  // < 0: fa_flash_fwd; else fa_flash_fwd_splitkv with this many ranges
 };
 
@@ -181,6 +186,8 @@ Options parse(int argc, char** argv) {
             if (o.splitkv < 0) throw std::invalid_argument("--splitkv must be >= 0");
         } else if (s == "--std") {
             o.std = std::stof(value());
+        } else if (s == "--sink") {
+            o.sink = std::stof(value());
         } else if (s == "--boost-keys") {
             const std::string v = value();
             const auto colon = v.find(':');
@@ -240,6 +247,15 @@ int run(const Options& o) {
                     row[c] = static_cast<_Float16>(static_cast<float>(row[c]) * o.boost);
                 }
             }
+        }
+    }
+
+    if (o.sink != 0.0F) {
+        const size_t nbh = static_cast<size_t>(o.batch) * o.heads;
+        for (size_t r = 0; r < nbh * o.seqlen; ++r) hq[r * o.head_dim] = static_cast<_Float16>(4.0F);
+        for (size_t bh = 0; bh < nbh; ++bh) {
+            hk[bh * o.seqlen * o.head_dim] =
+                static_cast<_Float16>(o.sink * std::sqrt(static_cast<float>(o.head_dim)) / 4.0F);
         }
     }
 
@@ -376,7 +392,7 @@ int main(int argc, char** argv) {
     } catch (const std::invalid_argument& e) {
         std::fprintf(stderr,
                      "error: %s\nusage: fa_dev [B H N D causal iters variant] [--lib PATH] "
-                     "[--warmup-ms MS] [--seed S] [--json] [--std X] [--boost-keys FRAC:FAC] "
+                     "[--warmup-ms MS] [--seed S] [--json] [--std X] [--boost-keys FRAC:FAC] [--sink NATS] "
                      "[--splitkv S]\n",
                      e.what());
         return 2;

@@ -145,7 +145,8 @@ typedef struct fa_tile_info {
 } fa_tile_info;
 int fa_tile_config(const fa_params* params, fa_tile_info* out);
 
-/* Library version string, e.g. "fa_hip 0.1.0 gfx950". */
+/* Library version string and softmax build options, e.g.
+ * "fa_hip 0.2.0 gfx950 pp16_unchecked=1 pp16_margin=0". */
 const char* fa_version(void);
 
 #ifdef __cplusplus

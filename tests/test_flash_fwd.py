@@ -140,8 +140,8 @@ def test_overflow_recompute(d, causal):
 def test_wide_score_spread(causal):
     """q, k ~ N(0, 1.9^2): scores of standard deviation about 5 in exp2 units, whose row maxima
     rise far above the first key tile's. The ping-pong kernels' unchecked tiles then run
-    against the first tile's max raised by the margin, with most p as fp16 subnormals, and
-    some items take the second pass: fp64 rows at the north-star tolerance."""
+    against the first tile's max, many p overflow fp16 and many items take the second pass:
+    fp64 rows at the north-star tolerance."""
     b, h, n, d = 4, 16, 4096, 128
     print(f"case spread B={b} H={h} N={n} causal={causal}", flush=True)
     q, k, v = _qkv(b, h, n, d, seed=14)
@@ -151,6 +151,39 @@ def test_wide_score_spread(causal):
     for bh in (0, 21, b * h - 1):
         ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, causal, bh, rows)).float()
         _close(out.view(b * h, n, d)[bh, rows], ref)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_sink(d, causal):
+    """Key 0 about 13 nats above every other key for every query (an attention sink), 16 heads
+    of 16384 keys: the ping-pong rows take p against the first key tile's max, which here is
+    the sink's, and the other keys' ~6 % of each row's weight lies 17-20 exp2 units below it.
+    A reference max raised above the sink would flush that mass with no second pass
+    (tests/test_softmax_model.py); the kernel must keep it. d=128: every row of every head
+    against the fp32 oracle; d=64: fp64 rows at the start, middle and end of three heads.
+    Then the split-KV launch of two heads (its range 0 runs the same first-tile arithmetic)."""
+    from fa import native
+    from test_softmax_model import sink_qkv
+
+    b, h, n = 1, 16, 16384
+    t = native.tile_config(d, causal, "opt", n, b, h)
+    assert (t["block_q"], t["waves"]) == (256, 8), t  # the ping-pong rows
+    print(f"case sink B={b} H={h} N={n} d={d} causal={causal}", flush=True)
+    q, k, v = sink_qkv(h, n, d, 13.0, seed=40 + d)
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    out = _fa().forward(qg, kg, vg, causal=causal).float().cpu()
+    if d == 128:
+        _close(out, orc.attention_fp32(q, k, v, causal=causal))
+    else:
+        rows = [0, 31, 255, 256, 4000, n // 2, n - 257, n - 1]
+        for bh in (0, 7, h - 1):
+            ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, causal, bh, rows)).float()
+            _close(out[0, bh, rows], ref)
+    q2, k2, v2 = (x[:, :2].contiguous() for x in (qg, kg, vg))
+    print(f"case sink split-KV B=1 H=2 N={n} d={d} causal={causal}", flush=True)
+    o_split, _ = _fa().forward_splitkv(q2, k2, v2, causal=causal)
+    _close(o_split, orc.attention_fp32(q2, k2, v2, causal=causal))
 
 
 @pytest.mark.parametrize("d", [64, 128])
