@@ -816,7 +816,7 @@ using PP16ReadSched = std::conditional_t<
 #endif
 // The unchecked run tests for an overflow at the boundaries of chunks of 1, 2, 4, ... steps of
 // three tiles, at most FA_PP16_EXIT_STEPS steps long (outside its inner loop, which stays the
-// plain three-tile body).
+// plain three-tile body); 0 runs it as one chunk, i.e. without the early exit.
 #ifndef FA_PP16_EXIT_STEPS
 #define FA_PP16_EXIT_STEPS 32
 #endif
@@ -1554,7 +1554,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 }
                 const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
                 if (exit_ok && wave_any(bad) && lane == 0) flags[slot] = 1;
-                const int chunk_end = min(n_free, jj + 3 * chunk);
+                const int chunk_end =
+                    FA_PP16_EXIT_STEPS > 0 ? min(n_free, jj + 3 * chunk) : n_free;
                 for (; jj + 3 <= chunk_end; jj += 3) {
                     tile(jj, I1{}, Unchecked{});
                     tile(jj + 1, I2{}, Unchecked{});

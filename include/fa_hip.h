@@ -61,8 +61,11 @@ typedef struct fa_params {
 /* Launches the forward kernel asynchronously on `stream` (a hipStream_t; NULL = the null
  * stream) on the current HIP device and returns without synchronizing. All argument checks
  * run before any HIP call, so FA_EINVAL never touches the device. Writes only rows < N of o.
- * Allocates nothing; re-entrant. Faults during execution surface at the caller's next
- * synchronization, as with any asynchronous HIP launch.
+ * Allocates nothing per call; re-entrant. (The library's code object holds the 64 MiB scratch
+ * array of fa_flash_fwd_splitkv_static below, FA_STATIC_SCRATCH_BYTES, so a process that
+ * launches any of its kernels on a GPU holds that much device memory there until it ends.)
+ * Faults during execution surface at the caller's next synchronization, as with any
+ * asynchronous HIP launch.
  * Replaces fa::flash_fwd (csrc/flash_fwd.h:33; checks at csrc/kernels/flash_fwd.cu:626-651). */
 int fa_flash_fwd(const fa_params* params, void* stream);
 
