@@ -124,6 +124,34 @@ def _v_read_offsets(geo, d, nb, h, db, e):
     return out
 
 
+def _tr16_received(offs, g0):
+    """Byte addresses whose halves lane g0 + j receives (element i = 0..3) from one
+    ds_read_b64_tr_b16 of the 16-lane group g0..g0+15, lane m having addressed the 4 halves at
+    offs[m]: element i of lane j is half j % 4 of lane 4i + j // 4's address. This is the
+    instruction's lane semantic as measured on MI355X (tests/test_blocks.py::
+    test_tr16_lane_mapping: with lane m addressing halves 4m..4m+3 of a counting tile, lane j
+    receives 16i + j)."""
+    return [[offs[g0 + 4 * i + j // 4] + 2 * (j % 4) for i in range(4)] for j in range(16)]
+
+
+def test_tr16_model_reproduces_the_gpu_probe():
+    """_tr16_received on the probe's addressing (lane m of the wave: halves 4m..4m+3 of a
+    counting tile) gives what tests/test_blocks.py::test_tr16_lane_mapping measures on the GPU:
+    lane l receives 64 (l // 16) + 16 i + l % 16."""
+    offs = [8 * m for m in range(64)]
+    for g0 in range(0, 64, 16):
+        for j, addrs in enumerate(_tr16_received(offs, g0)):
+            l = g0 + j
+            assert [a // 2 for a in addrs] == [64 * (l // 16) + 16 * i + l % 16 for i in range(4)]
+
+
+def _logical(geo, addr, rb, m16=False, d=None):
+    """(row, half column) of the logical tile element stored at byte `addr`."""
+    row, phys = addr // rb, (addr % rb) // 16
+    chunk = geo.geom_swizzle_chunk_m16(row, phys, d) if m16 else geo.geom_swizzle_chunk(row, phys, rb)
+    return row, 8 * chunk + (addr % 16) // 2
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_v_transposed_reads_are_conflict_free(geo, d):
     for nb, h, db, e in itertools.product(range(2), range(2), range(d // 32), range(2)):
@@ -153,12 +181,12 @@ def test_v_transposed_reads_deliver_the_pv_keys(geo, d):
             assert len(rows) == 4 and rows == list(range(rows[0], rows[0] + 4))
             cols = sorted({c + j for _, c in cells for j in range(4)})
             assert cols == list(range(cols[0], cols[0] + 16))
-            # the transpose hands lane g0+j column cols[0]+j of rows[0..3]
-            for j in range(16):
+            # what each lane receives, through the instruction's lane semantic
+            for j, addrs in enumerate(_tr16_received(offs, g0)):
                 lane = g0 + j
-                assert cols[0] + j == 32 * db + (lane % 32)
-                for i in range(4):
-                    assert rows[i] == 32 * nb + 16 * h + geo.geom_pv_key(lane, 4 * e + i)
+                for i, addr in enumerate(addrs):
+                    assert _logical(geo, addr, rb) == (
+                        32 * nb + 16 * h + geo.geom_pv_key(lane, 4 * e + i), 32 * db + lane % 32)
 
 
 @pytest.mark.parametrize("d", [64, 128])
@@ -288,11 +316,11 @@ def test_m16_v_transposed_reads_deliver_the_pv16_keys(geo, d):
             assert len(rows) == 4 and rows == list(range(rows[0], rows[0] + 4))
             cols = sorted({col + j for _, col in cells for j in range(4)})
             assert cols == list(range(cols[0], cols[0] + 16))
-            for j in range(16):
+            for j, addrs in enumerate(_tr16_received(offs, g0)):
                 lane = g0 + j
-                assert cols[0] + j == 16 * db + lane % 16
-                for i in range(4):
-                    assert rows[i] == geo.geom_pv16_key(lane, t, 4 * e + i)
+                for i, addr in enumerate(addrs):
+                    assert _logical(geo, addr, rb, True, d) == (
+                        geo.geom_pv16_key(lane, t, 4 * e + i), 16 * db + lane % 16)
 
 
 @pytest.mark.parametrize("d", [64, 128])
@@ -545,3 +573,67 @@ def test_causal_pairs_choice_against_a_list_schedule(geo):
                 assert singles <= 0.99 * pairs, (bhc, nqb, pairs, singles)
             elif singles < 0.95 * pairs:
                 pytest.fail(f"pairs kept at {(bhc, nqb)}: {pairs} vs {singles}")
+
+
+# ---- mutation check of the layout tests above ---------------------------------------------------
+# Counterpart of the reference's planted-bug check of its building-block tests
+# (docs/testing.md:64-74: removing the swizzle XOR and a wrong ldmatrix lane map each failed a
+# unit test). Here the same two mistakes are planted in a stand-in for the geometry library --
+# the real functions, except the mutated ones, which are written out below -- and fed through
+# the conflict and lane-map checks of this file, each of which must then fail.
+
+
+class _Mutant:
+    def __init__(self, geo, **over):
+        self._geo, self._over = geo, over
+
+    def __getattr__(self, name):
+        return self._over.get(name, getattr(self._geo, name))
+
+
+def _unswizzled(geo):
+    """No row XOR in either layout: chunk c of row r at byte r * row_bytes + 16 c."""
+    return _Mutant(
+        geo,
+        geom_row_xor=lambda row, rb: 0,
+        geom_swizzle_chunk=lambda row, chunk, rb: chunk,
+        geom_tile_offset=lambda row, chunk, rb: row * rb + 16 * chunk,
+        geom_row_xor_m16=lambda row, d: 0,
+        geom_swizzle_chunk_m16=lambda row, chunk, d: chunk,
+        geom_tile_offset_m16=lambda row, chunk, d: row * 2 * d + 16 * chunk,
+    )
+
+
+def _tr16_transposed(geo):
+    """The transposing read's lane map with row and column roles swapped: lane l addresses row
+    l % 4 and column 4 * ((l % 16) // 4) instead of row (l % 16) // 4 and column 4 (l % 4)."""
+    return _Mutant(geo, geom_tr16_row=lambda lane: lane & 3,
+                   geom_tr16_col=lambda lane: 4 * ((lane & 15) >> 2))
+
+
+@pytest.mark.parametrize("check", [test_k_fragment_reads_are_conflict_free,
+                                   test_v_transposed_reads_are_conflict_free,
+                                   test_m16_v_transposed_reads_are_conflict_free])
+def test_unswizzled_layout_is_caught(geo, check):
+    with pytest.raises(AssertionError):
+        check(_unswizzled(geo), 128)
+
+
+@pytest.mark.parametrize("check", [test_v_transposed_reads_deliver_the_pv_keys,
+                                   test_m16_v_transposed_reads_deliver_the_pv16_keys])
+def test_wrong_tr16_lane_map_is_caught(geo, check):
+    for d in (64, 128):
+        with pytest.raises(AssertionError):
+            check(_tr16_transposed(geo), d)
+
+
+def test_mutants_leave_the_checks_green_on_the_real_layout(geo):
+    """The checks above pass through the stand-in when nothing is mutated, so a failure under
+    a mutant is the mutant's doing."""
+    same = _Mutant(geo)
+    for d in (64, 128):
+        test_k_fragment_reads_are_conflict_free(same, d)
+        test_v_transposed_reads_are_conflict_free(same, d)
+        test_m16_v_transposed_reads_are_conflict_free(same, d)
+        test_v_transposed_reads_deliver_the_pv_keys(same, d)
+        test_m16_v_transposed_reads_deliver_the_pv16_keys(same, d)
