@@ -72,11 +72,19 @@ namespace g = fa::geom;
 #endif
 
 // Main-loop schedules: SIMPLE (flash_fwd_kernel: each wave runs QK, softmax and PV of a tile in
-// turn), KSPLIT (flash_fwd_ksplit: two waves per 32 query rows on alternate key tiles),
+// turn), KSPLIT / KSPLIT4 (flash_fwd_ksplit: two or four waves per 32 query rows, each on every
+// second or fourth key tile),
 // PINGPONG16 (flash_fwd_pingpong16: two groups of waves alternate between an MFMA-only phase and
 // a softmax phase, on 16x16x32 MFMAs; the table's long d = 128 rows). The values are those the
 // -D tile overrides name.
-enum Sched { SIMPLE = 0, KSPLIT = 3, PINGPONG16 = 4 };
+enum Sched { SIMPLE = 0, KSPLIT = 3, PINGPONG16 = 4, KSPLIT4 = 5 };
+
+// K/V buffers of the simple schedule: 2 (refill one tile ahead, wait for all DMA at each tile)
+// or 3 (two tiles ahead; a tile waits only for its own DMA, the next tile's stays in flight).
+#ifndef FA_SIMPLE_NBUF
+#define FA_SIMPLE_NBUF 2
+#endif
+static_assert(FA_SIMPLE_NBUF == 2 || FA_SIMPLE_NBUF == 3, "two or three K/V buffers");
 
 template <int D_, int BC_, int NW_, bool LAZY_, int SCHED_>
 struct Tile {
@@ -86,13 +94,16 @@ struct Tile {
     static constexpr bool LAZY = LAZY_;     // rescale O only when a row max grows by > 2^8
     static constexpr int SCHED = SCHED_;    // main-loop schedule (Sched)
     static constexpr int BR = 32 * NW;      // query rows per workgroup
-    static constexpr int KS = SCHED == KSPLIT ? 2 : 1;  // waves per 32 query rows (key halves)
+    static constexpr int KS =  // waves per 32 query rows (key parts)
+        SCHED == KSPLIT ? 2 : (SCHED == KSPLIT4 ? 4 : 1);
     static constexpr int THREADS = 64 * NW * KS;
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
     static constexpr bool M16 = SCHED == PINGPONG16;      // 16x16x32 layouts
-    static constexpr int NBUF = SCHED == PINGPONG16 ? 3 : 2;  // per K, V
+    static constexpr int NBUF =  // per K, V (the simple schedule's third only within 64 KiB)
+        SCHED == PINGPONG16 ? 3
+                            : (SCHED == SIMPLE && 6 * TILE_BYTES <= 64 * 1024 ? FA_SIMPLE_NBUF : 2);
     static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES * KS;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
@@ -101,7 +112,7 @@ struct Tile {
     static_assert(D == 64 || D == 128, "head dim must be 64 or 128");
     static_assert(BC % 32 == 0, "BC must be a multiple of the 32-key MFMA block");
     static_assert((BC * CPR) % (64 * NW) == 0, "tile must split evenly over the waves");
-    static_assert(LDS_BYTES <= 64 * 1024, "static LDS budget");
+    static_assert(LDS_BYTES <= (KS == 4 ? 160 : 64) * 1024, "static LDS budget");
 };
 
 // DMA plan of one wave for a K or V tile: DMA_ITERS 16-byte-per-lane buffer->LDS copies, each
@@ -409,13 +420,16 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
     float* __restrict__ lse_part) {
     // One LDS object per buffer, and the buffer of each tile fixed at compile time (the loop is
-    // unrolled by two): the compiler then sees that the refill of one buffer cannot alias the
-    // reads of the other and waits for a tile's DMA only at the barrier that starts the tile.
-    // With one array it would wait for the next tile's refill before this tile's P.V reads.
+    // unrolled by the buffer count): the compiler then sees that the refill of one buffer cannot
+    // alias the reads of another and waits for a tile's DMA only at the barrier that starts the
+    // tile. With one array it would wait for the next tile's refill before this tile's P.V reads.
+    constexpr int NBUF = T::NBUF;
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds2[T::TILE_BYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
@@ -438,19 +452,27 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     // plain one the extra exit costs the causal d=64 tile 30 VGPRs (and half its occupancy).
     if (SPLIT && range.count == 0) return;
 
-    // Tile t lives in buffer t % 2.
+    // Tile j lives in buffer (j - j_begin) % NBUF.
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    auto kbuf = [&](auto b) { return decltype(b)::value == 0 ? k_lds0 : k_lds1; };
-    auto vbuf = [&](auto b) { return decltype(b)::value == 0 ? v_lds0 : v_lds1; };
+    using I2 = std::integral_constant<int, 2>;
+    auto kbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? k_lds0 : (B == 1 ? k_lds1 : k_lds2);
+    };
+    auto vbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? v_lds0 : (B == 1 ? v_lds1 : v_lds2);
+    };
 
     const TileDma<T> dma(wave, lane);
-    if (j_begin & 1) {
-        load_tile<T>(kh, j_begin * T::BC, n, kbuf(I1{}), dma);
-        load_tile<T>(vh, j_begin * T::BC, n, vbuf(I1{}), dma);
-    } else {
-        load_tile<T>(kh, j_begin * T::BC, n, kbuf(I0{}), dma);
-        load_tile<T>(vh, j_begin * T::BC, n, vbuf(I0{}), dma);
+    load_tile<T>(kh, j_begin * T::BC, n, kbuf(I0{}), dma);
+    load_tile<T>(vh, j_begin * T::BC, n, vbuf(I0{}), dma);
+    if constexpr (NBUF == 3) {
+        if (j_begin + 1 < n_tiles) {
+            load_tile<T>(kh, (j_begin + 1) * T::BC, n, kbuf(I1{}), dma);
+            load_tile<T>(vh, (j_begin + 1) * T::BC, n, vbuf(I1{}), dma);
+        }
     }
     f16x8 qf[T::KK];
     load_q<T>(q + head, qrow, n, lane, negate_q, qf);
@@ -462,16 +484,23 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     float m_run = -INFINITY;  // running max of this lane's query, log2 domain (scaled)
     float l_run = 0.0F;       // this lane's partial row sum (its 16 keys of each 32-key block)
 
-    // Tile j in buffer B = j % 2: barrier, refill of the other buffer with tile j+1, then
-    // S = QK^T, mask, softmax and O += PV.
+    // Tile j in buffer B: its DMA landed (with three buffers the next tile's may still be in
+    // flight: its 2 * DMA_ITERS requests are the newest), barrier, refill of the buffer read by
+    // the previous tile with tile j + NBUF - 1, then S = QK^T, mask, softmax and O += PV.
     auto tile = [&](int j, auto b) {
         constexpr int B = decltype(b)::value;
-        using Other = std::integral_constant<int, 1 - B>;
-        wait_vmem();
+        using Refill = std::integral_constant<int, (B + NBUF - 1) % NBUF>;
+        if (NBUF == 3 && j > j_begin && j + 1 < n_tiles) {
+            // vmcnt(2 * DMA_ITERS) lgkmcnt(0): only the next tile's requests stay in flight
+            // (the first tile also waits for the Q loads issued after its DMA)
+            __builtin_amdgcn_s_waitcnt(static_cast<short>(0x0070 | (2 * T::DMA_ITERS)));
+        } else {
+            wait_vmem();
+        }
         __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
-        if (j + 1 < n_tiles) {
-            load_tile<T>(kh, (j + 1) * T::BC, n, kbuf(Other{}), dma);
-            load_tile<T>(vh, (j + 1) * T::BC, n, vbuf(Other{}), dma);
+        if (j + NBUF - 1 < n_tiles) {
+            load_tile<T>(kh, (j + NBUF - 1) * T::BC, n, kbuf(Refill{}), dma);
+            load_tile<T>(vh, (j + NBUF - 1) * T::BC, n, vbuf(Refill{}), dma);
         }
         const int kt = j * T::BC;
         if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) return;  // wave-uniform
@@ -483,15 +512,21 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         pv_tile<T>(vbuf(b), fr, p, oacc);
     };
     int j = j_begin;
-    if (j & 1) {
-        tile(j, I1{});
-        ++j;
+    if constexpr (NBUF == 3) {
+        for (; j + 3 <= n_tiles; j += 3) {
+            tile(j, I0{});
+            tile(j + 1, I1{});
+            tile(j + 2, I2{});
+        }
+        if (j < n_tiles) tile(j, I0{});
+        if (j + 1 < n_tiles) tile(j + 1, I1{});
+    } else {
+        for (; j + 2 <= n_tiles; j += 2) {
+            tile(j, I0{});
+            tile(j + 1, I1{});
+        }
+        if (j < n_tiles) tile(j, I0{});
     }
-    for (; j + 2 <= n_tiles; j += 2) {
-        tile(j, I0{});
-        tile(j + 1, I1{});
-    }
-    if (j < n_tiles) tile(j, I0{});
     if constexpr (SPLIT) {
         const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
         store_partial<T>(o_part + part * n * T::D, lse_part + part * n, qrow, n, lane, m_run,
@@ -553,36 +588,47 @@ __global__ __launch_bounds__(256) void flash_fwd_combine(
 }
 
 // ---- kernel, key-split schedule (small grids) --------------------------------------------------
-// Two waves per 32 query rows: wave w < NW takes the even key tiles of the query block and wave
-// w + NW the odd ones, each with its own running max, row sum and O (simple schedule per
-// tile); at the end the odd half hands (m, l, O) to the even half through LDS, which merges
-// them (O = 2^(m_a - m) O_a + 2^(m_b - m) O_b, l likewise) and stores. Twice the waves of the
-// simple schedule on the same grid, for grids too small to fill the GPU, with no workspace.
+// KS waves per 32 query rows (KS = 2, or 4 for grids of one workgroup per CU): wave w takes key
+// tiles part, part + KS, part + 2 KS, ... of the query block (part = w / NW), each with its own
+// running max, row sum and O (simple schedule per tile). At the end the parts merge pairwise
+// through LDS in log2(KS) rounds, part p + d handing (m, l, O) to part p (d = KS/2, ..., 1),
+// which merges them (O = 2^(m_a - m) O_a + 2^(m_b - m) O_b, l likewise); part 0 stores. KS times
+// the waves of the simple schedule on the same grid, for grids too small to fill the GPU, with
+// no workspace.
 template <class T, bool CAUSAL>
 __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
     float* /*lse_part*/) {
-    static_assert(T::KS == 2, "two key halves");
-    // One LDS object per (key half, buffer) for K and V, and the buffer of each step fixed at
+    constexpr int KS = T::KS;
+    static_assert(KS == 2 || KS == 4, "two or four key parts");
+    // One LDS object per (key part, buffer) for K and V, and the buffer of each step fixed at
     // compile time (the step loop is unrolled by two): the compiler then sees that a refill
     // cannot alias the reads of the other buffer and waits for DMA only at the step barrier.
-    // Two of the objects are reused by the merge at the end.
+    // (Parts 2 and 3 exist only with KS = 4.) The merge reuses buffer 0 of each part.
     __shared__ __attribute__((aligned(1024))) char k00[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k01[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k10[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k11[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k20[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k21[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k30[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k31[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v00[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v01[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v10[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char v11[T::TILE_BYTES];
-    static_assert(T::NW * 128 * 4 <= T::TILE_BYTES && T::NW * 64 * 16 * 4 <= T::TILE_BYTES,
+    __shared__ __attribute__((aligned(1024))) char v20[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v21[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v30[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v31[T::TILE_BYTES];
+    static_assert(T::NW * 64 * 8 <= T::TILE_BYTES && T::NW * 64 * 16 * 4 <= T::TILE_BYTES,
                   "the merge's (m, l) and O blocks fit in one tile buffer each");
 
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
-    const int half = wave / T::NW;  // 0: even key tiles, 1: odd key tiles
+    const int part = wave / T::NW;  // key tiles part, part + KS, ...
     const int wq = wave % T::NW;    // which 32 query rows
     const g::Work w = g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
@@ -592,29 +638,44 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const int qw = q0 + wq * 32;
     const int qrow = qw + (lane & 31);
     const int n_tiles = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
-    const int n_steps = (n_tiles + 1) / 2;
+    const int n_steps = (n_tiles + KS - 1) / KS;
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    // Buffer b of key half H (both compile-time).
+    // Buffer b of key part H (both compile-time).
     auto kbuf = [&](auto hc, auto b) {
         constexpr int H = decltype(hc)::value;
-        return decltype(b)::value == 0 ? (H ? k10 : k00) : (H ? k11 : k01);
+        constexpr int B = decltype(b)::value;
+        if constexpr (H == 0) return B == 0 ? k00 : k01;
+        else if constexpr (H == 1) return B == 0 ? k10 : k11;
+        else if constexpr (H == 2) return B == 0 ? k20 : k21;
+        else return B == 0 ? k30 : k31;
     };
     auto vbuf = [&](auto hc, auto b) {
         constexpr int H = decltype(hc)::value;
-        return decltype(b)::value == 0 ? (H ? v10 : v00) : (H ? v11 : v01);
+        constexpr int B = decltype(b)::value;
+        if constexpr (H == 0) return B == 0 ? v00 : v01;
+        else if constexpr (H == 1) return B == 0 ? v10 : v11;
+        else if constexpr (H == 2) return B == 0 ? v20 : v21;
+        else return B == 0 ? v30 : v31;
+    };
+    // Calls f with the wave's part as a compile-time constant (wave-uniform branch).
+    auto with_part = [&](auto&& f) {
+        if constexpr (KS == 4) {
+            if (part == 3) return f(std::integral_constant<int, 3>{});
+            if (part == 2) return f(std::integral_constant<int, 2>{});
+        }
+        if (part == 1) return f(I1{});
+        return f(I0{});
     };
 
     const TileDma<T> dma(wq, lane);
-    if (half < n_tiles) {
-        if (half) {
-            load_tile<T>(kh, T::BC, n, kbuf(I1{}, I0{}), dma);
-            load_tile<T>(vh, T::BC, n, vbuf(I1{}, I0{}), dma);
-        } else {
-            load_tile<T>(kh, 0, n, kbuf(I0{}, I0{}), dma);
-            load_tile<T>(vh, 0, n, vbuf(I0{}, I0{}), dma);
+    with_part([&](auto hc) {
+        constexpr int H = decltype(hc)::value;
+        if (H < n_tiles) {
+            load_tile<T>(kh, H * T::BC, n, kbuf(hc, I0{}), dma);
+            load_tile<T>(vh, H * T::BC, n, vbuf(hc, I0{}), dma);
         }
-    }
+    });
     f16x8 qf[T::KK];
     load_q<T>(q + head, qrow, n, lane, negate_q, qf);
     const Frag<T> fr(lane);
@@ -625,18 +686,18 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     float m_run = -INFINITY;
     float l_run = 0.0F;
 
-    // Step j in buffer B = j % 2: key half H's tile 2j + H.
+    // Step j in buffer B = j % 2: key part H's tile KS j + H.
     auto step = [&](int j, auto hc, auto b) {
         constexpr int H = decltype(hc)::value;
         using Other = std::integral_constant<int, 1 - decltype(b)::value>;
         wait_vmem();
         __syncthreads();  // step j's tiles are in LDS; step j-1's buffers are free
-        const int tn = 2 * (j + 1) + H;
+        const int tn = KS * (j + 1) + H;
         if (tn < n_tiles) {
             load_tile<T>(kh, tn * T::BC, n, kbuf(hc, Other{}), dma);
             load_tile<T>(vh, tn * T::BC, n, vbuf(hc, Other{}), dma);
         }
-        const int t = 2 * j + H;
+        const int t = KS * j + H;
         const int kt = t * T::BC;
         if (t >= n_tiles || qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) return;
         f32x16 s[T::NB];
@@ -646,65 +707,87 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
         softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
         pv_tile<T>(vbuf(hc, b), fr, p, oacc);
     };
-    auto steps = [&](auto hc) {
+    // wave-uniform branch; every part passes the same number of barriers
+    with_part([&](auto hc) {
         int j = 0;
         for (; j + 2 <= n_steps; j += 2) {
             step(j, hc, I0{});
             step(j + 1, hc, I1{});
         }
         if (j < n_steps) step(j, hc, I0{});
-    };
-    if (half) {  // wave-uniform; both halves pass the same number of barriers
-        steps(I1{});
-    } else {
-        steps(I0{});
-    }
+    });
 
-    // Merge through LDS: (m, l) of the odd half, then O one 32-column block at a time.
-    const float l_tot = sum_xor32(l_run);
-    float* ml = reinterpret_cast<float*>(k00);        // [NW][64][2]
-    float* ob = reinterpret_cast<float*>(v00);        // [NW][64][16]
+    // Merge. In round d (d = KS/2, ..., 1), part p + d (p < d) writes (m, l) to its buffer k_0
+    // and then O, one 32-column block at a time, to its buffer v_0; part p merges. Lanes write
+    // 8 and 16 bytes at consecutive addresses (O as four 16-byte pieces per block, piece-major),
+    // which keeps every access free of bank conflicts.
+    float l_tot = sum_xor32(l_run);
     const int slot = wq * 64 + lane;
     wait_vmem();
     __syncthreads();  // every wave is done with the tile buffers
-    if (half == 1) {
-        ml[2 * slot] = m_run;
-        ml[2 * slot + 1] = l_tot;
-    }
-    __syncthreads();
-    float m_new = m_run, wa = 1.0F, wb = 0.0F, l_new = l_tot;
-    if (half == 0) {
-        const float mb = ml[2 * slot];
-        const float lb = ml[2 * slot + 1];
-        m_new = fmaxf(m_run, mb);
-        // a half that saw no key has m = -inf and weighs 0; both -inf only for rows >= n
-        wa = m_run == -INFINITY ? 0.0F : exp2_fast(m_run - m_new);
-        wb = mb == -INFINITY ? 0.0F : exp2_fast(mb - m_new);
-        l_new = l_tot * wa + lb * wb;
-    }
 #pragma unroll
-    for (int db = 0; db < T::DB; ++db) {
-        if (half == 1) {
-#pragma unroll
-            for (int r = 0; r < 16; r += 4) {
-                *reinterpret_cast<f32x4*>(ob + 16 * slot + r) =
-                    f32x4{oacc[db][r], oacc[db][r + 1], oacc[db][r + 2], oacc[db][r + 3]};
+    for (int d = KS / 2; d >= 1; d /= 2) {
+        const bool sender = part >= d && part < 2 * d;
+        const bool receiver = part < d;
+        // buffers k_0 and v_0 of part src (1, 2 or 3: a sender), read by its receiver too
+        auto ml_of = [&](int src) -> float* {
+            if constexpr (KS == 4) {
+                if (src == 3) return reinterpret_cast<float*>(k30);
+                if (src == 2) return reinterpret_cast<float*>(k20);
             }
+            return reinterpret_cast<float*>(k10);
+        };
+        auto ob_of = [&](int src) -> float* {
+            if constexpr (KS == 4) {
+                if (src == 3) return reinterpret_cast<float*>(v30);
+                if (src == 2) return reinterpret_cast<float*>(v20);
+            }
+            return reinterpret_cast<float*>(v10);
+        };
+        if (sender) {
+            *reinterpret_cast<f32x2*>(ml_of(part) + 2 * slot) = f32x2{m_run, l_tot};
         }
         __syncthreads();
-        if (half == 0) {
-#pragma unroll
-            for (int r = 0; r < 16; r += 4) {
-                const f32x4 x = *reinterpret_cast<const f32x4*>(ob + 16 * slot + r);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) oacc[db][r + i] = oacc[db][r + i] * wa + x[i] * wb;
-            }
+        float wa = 1.0F, wb = 0.0F;
+        if (receiver) {
+            const f32x2 mb_lb = *reinterpret_cast<const f32x2*>(ml_of(part + d) + 2 * slot);
+            const float mb = mb_lb[0];
+            const float m_new = fmaxf(m_run, mb);
+            // a part that saw no key has m = -inf and weighs 0; both -inf only for rows >= n
+            wa = m_run == -INFINITY ? 0.0F : exp2_fast(m_run - m_new);
+            wb = mb == -INFINITY ? 0.0F : exp2_fast(mb - m_new);
+            l_tot = l_tot * wa + mb_lb[1] * wb;
+            m_run = m_new;
         }
-        __syncthreads();
+#pragma unroll
+        for (int db = 0; db < T::DB; ++db) {
+            if (sender) {
+                float* ob = ob_of(part);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    *reinterpret_cast<f32x4*>(ob + 4 * (r * T::NW * 64 + slot)) =
+                        f32x4{oacc[db][4 * r], oacc[db][4 * r + 1], oacc[db][4 * r + 2],
+                              oacc[db][4 * r + 3]};
+                }
+            }
+            __syncthreads();
+            if (receiver) {
+                const float* ob = ob_of(part + d);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(ob + 4 * (r * T::NW * 64 + slot));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        oacc[db][4 * r + i] = oacc[db][4 * r + i] * wa + x[i] * wb;
+                    }
+                }
+            }
+            __syncthreads();
+        }
     }
-    if (half == 0) {
+    if (part == 0) {
         store_o_tot<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qrow, n,
-                       lane, m_new, l_new, oacc);
+                       lane, m_run, l_tot, oacc);
     }
 }
 
@@ -1728,6 +1811,24 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #ifndef FA_OPT_D128_SMALL
 #define FA_OPT_D128_SMALL 32, 2, true, KSPLIT
 #endif
+// Grids of at most FA_TINY_GRID_WGS 64-row query blocks (one round of one workgroup per CU)
+// whose key loop has at least FA_TINY_MIN_TILES tiles: four waves per 32 query rows, each on
+// every fourth key tile (128 KiB of LDS, eight waves). Against the two-way split, interleaved on
+// one box: 1x8x2048 d=64 causal +12.7 %, 2x4x1500 d=128 causal +11.8 %, 2x8x1000 d=128 causal
+// +4.5 %, 1x16x1024 d=128 +1.7 %, 2x8x1000 d=64 causal (16 tiles) +1.9 %; with 8 tiles
+// (4x8x500 d=64) -7.7 %, with 4 (1x4x256 d=64) -13.8 %.
+#ifndef FA_OPT_D64_TINY
+#define FA_OPT_D64_TINY 64, 2, true, KSPLIT4
+#endif
+#ifndef FA_OPT_D128_TINY
+#define FA_OPT_D128_TINY 32, 2, true, KSPLIT4
+#endif
+#ifndef FA_TINY_GRID_WGS
+#define FA_TINY_GRID_WGS 256
+#endif
+#ifndef FA_TINY_MIN_TILES
+#define FA_TINY_MIN_TILES 16
+#endif
 #ifndef FA_OPT_D64
 #define FA_OPT_D64 64, 8, true, SIMPLE
 #endif
@@ -1777,6 +1878,7 @@ struct Entry {
 enum TileId : int {
     BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
     OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
+    OPT_D64_TINY, OPT_D64_C_TINY, OPT_D128_TINY, OPT_D128_C_TINY,
     OPT_D64, OPT_D64_C, OPT_D64_LONG, OPT_D64_C_LONG, OPT_D128_SHORT, OPT_D128, OPT_D128_C_SHORT,
     OPT_D128_C,
 };
@@ -1789,6 +1891,10 @@ template <> struct Row<OPT_D64_SMALL> : Entry<Tile<64, FA_OPT_D64_SMALL>, false>
 template <> struct Row<OPT_D64_C_SMALL> : Entry<Tile<64, FA_OPT_D64_SMALL>, true> {};
 template <> struct Row<OPT_D128_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, false> {};
 template <> struct Row<OPT_D128_C_SMALL> : Entry<Tile<128, FA_OPT_D128_SMALL>, true> {};
+template <> struct Row<OPT_D64_TINY> : Entry<Tile<64, FA_OPT_D64_TINY>, false> {};
+template <> struct Row<OPT_D64_C_TINY> : Entry<Tile<64, FA_OPT_D64_TINY>, true> {};
+template <> struct Row<OPT_D128_TINY> : Entry<Tile<128, FA_OPT_D128_TINY>, false> {};
+template <> struct Row<OPT_D128_C_TINY> : Entry<Tile<128, FA_OPT_D128_TINY>, true> {};
 template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
 template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
 template <> struct Row<OPT_D64_LONG> : Entry<Tile<64, FA_OPT_D64_LONG>, false> {};
@@ -1805,6 +1911,13 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
         return causal ? BASE_D128_C : BASE_D128;
     }
     if (bh * ((static_cast<int64_t>(n) + 255) / 256) < FA_SMALL_GRID_WGS) {
+        const int bc =
+            head_dim == 64 ? Tile<64, FA_OPT_D64_TINY>::BC : Tile<128, FA_OPT_D128_TINY>::BC;
+        if (bh * ((static_cast<int64_t>(n) + 63) / 64) <= FA_TINY_GRID_WGS &&
+            (n + bc - 1) / bc >= FA_TINY_MIN_TILES) {
+            if (head_dim == 64) return causal ? OPT_D64_C_TINY : OPT_D64_TINY;
+            return causal ? OPT_D128_C_TINY : OPT_D128_TINY;
+        }
         if (head_dim == 64) return causal ? OPT_D64_C_SMALL : OPT_D64_SMALL;
         return causal ? OPT_D128_C_SMALL : OPT_D128_SMALL;
     }
@@ -1836,6 +1949,10 @@ decltype(auto) with_row(TileId id, F&& f) {
         case OPT_D64_C_SMALL: return f(Row<OPT_D64_C_SMALL>{});
         case OPT_D128_SMALL: return f(Row<OPT_D128_SMALL>{});
         case OPT_D128_C_SMALL: return f(Row<OPT_D128_C_SMALL>{});
+        case OPT_D64_TINY: return f(Row<OPT_D64_TINY>{});
+        case OPT_D64_C_TINY: return f(Row<OPT_D64_C_TINY>{});
+        case OPT_D128_TINY: return f(Row<OPT_D128_TINY>{});
+        case OPT_D128_C_TINY: return f(Row<OPT_D128_C_TINY>{});
         case OPT_D64: return f(Row<OPT_D64>{});
         case OPT_D64_C: return f(Row<OPT_D64_C>{});
         case OPT_D64_LONG: return f(Row<OPT_D64_LONG>{});
@@ -1913,7 +2030,7 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
                 fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL, false, true>);
             }
         }
-    } else if constexpr (T::SCHED == KSPLIT) {
+    } else if constexpr (T::SCHED == KSPLIT || T::SCHED == KSPLIT4) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
     } else {
         fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL>);

@@ -7,12 +7,14 @@
             [--reps 3] [--csv PATH] [--bh B H] [--dev-args "--std 0.5 --boost-keys 0.01:8"]
 
 slot: one row of the tile table in csrc/flash_fwd.hip, named after its macro (see SLOTS):
-      opt_d64[_causal]_small, opt_d128[_causal]_small, opt_d64, opt_d64_causal,
+      opt_d64[_causal]_small, opt_d128[_causal]_small, opt_d64[_causal]_tiny,
+      opt_d128[_causal]_tiny, opt_d64, opt_d64_causal,
       opt_d128_short, opt_d128, opt_d128_causal_short, opt_d128_causal, base_d64, base_d128
 cand: "BC,NW,LAZY,SCHED" -- keys per tile, query waves per workgroup (BR = 32 * NW), lazy
-      rescale (true/false) and schedule (SIMPLE; KSPLIT, which runs two waves per query wave;
-      or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128, BC=64 at
-      D=64), e.g. 32,8,true,PINGPONG16. Without candidates a default list for the slot is used.
+      rescale (true/false) and schedule (SIMPLE; KSPLIT / KSPLIT4, which run two / four waves
+      per query wave; or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128,
+      BC=64 at D=64), e.g. 32,8,true,PINGPONG16. Without candidates a default list for the slot
+      is used.
 
 `build` compiles csrc/flash_fwd.hip once per candidate with the slot's macro overridden, into
 dev/_tune/<slot>/<cand>.so (candidates the tile checks reject fail to compile and are reported
@@ -49,12 +51,18 @@ TUNE = DEV / "_tune"
 # library's size thresholds so that the slot's row runs at every N and B*H of the sweep.
 _ALL, _NONE = "2147483647", "0"
 _BIG = [f"-DFA_SMALL_GRID_WGS={_NONE}"]
+_SMALL = [f"-DFA_SMALL_GRID_WGS={_ALL}", f"-DFA_TINY_GRID_WGS={_NONE}"]
+_TINY = [f"-DFA_SMALL_GRID_WGS={_ALL}", f"-DFA_TINY_GRID_WGS={_ALL}",
+         f"-DFA_TINY_MIN_TILES={_NONE}"]
 SLOTS = {
-    "opt_d64_small": ("FA_OPT_D64_SMALL", "opt", 64, 0, [f"-DFA_SMALL_GRID_WGS={_ALL}"]),
-    "opt_d64_causal_small": ("FA_OPT_D64_SMALL", "opt", 64, 1, [f"-DFA_SMALL_GRID_WGS={_ALL}"]),
-    "opt_d128_small": ("FA_OPT_D128_SMALL", "opt", 128, 0, [f"-DFA_SMALL_GRID_WGS={_ALL}"]),
-    "opt_d128_causal_small": ("FA_OPT_D128_SMALL", "opt", 128, 1,
-                              [f"-DFA_SMALL_GRID_WGS={_ALL}"]),
+    "opt_d64_small": ("FA_OPT_D64_SMALL", "opt", 64, 0, _SMALL),
+    "opt_d64_causal_small": ("FA_OPT_D64_SMALL", "opt", 64, 1, _SMALL),
+    "opt_d128_small": ("FA_OPT_D128_SMALL", "opt", 128, 0, _SMALL),
+    "opt_d128_causal_small": ("FA_OPT_D128_SMALL", "opt", 128, 1, _SMALL),
+    "opt_d64_tiny": ("FA_OPT_D64_TINY", "opt", 64, 0, _TINY),
+    "opt_d64_causal_tiny": ("FA_OPT_D64_TINY", "opt", 64, 1, _TINY),
+    "opt_d128_tiny": ("FA_OPT_D128_TINY", "opt", 128, 0, _TINY),
+    "opt_d128_causal_tiny": ("FA_OPT_D128_TINY", "opt", 128, 1, _TINY),
     "opt_d64": ("FA_OPT_D64", "opt", 64, 0, _BIG),
     "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1, _BIG),
     "opt_d128_short": ("FA_OPT_D128_SHORT", "opt", 128, 0, [*_BIG, f"-DFA_D128_SHORT_MAX_N={_ALL}"]),
@@ -68,9 +76,9 @@ SLOTS = {
 }
 DEFAULT_CANDS = {
     64: ["64,8,true,PINGPONG16", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE",
-         "64,4,false,SIMPLE", "64,2,true,KSPLIT", "32,2,true,KSPLIT"],
+         "64,4,false,SIMPLE", "64,2,true,KSPLIT", "32,2,true,KSPLIT", "64,2,true,KSPLIT4"],
     128: ["32,8,true,PINGPONG16", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE",
-          "64,4,false,SIMPLE", "32,2,true,KSPLIT", "32,4,true,KSPLIT"],
+          "64,4,false,SIMPLE", "32,2,true,KSPLIT", "32,4,true,KSPLIT", "32,2,true,KSPLIT4"],
 }
 
 

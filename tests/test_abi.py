@@ -111,11 +111,13 @@ def test_tile_config_invariants():
                 for n in (1, 1000, 2048, 2049, 3072, 3073, 4096, 4097, 8192, 8193, 16384):
                     for b, h in ((1, 1), (2, 8), (16, 32)):
                         bq, bk, waves, lds = _tile(d, causal, var, n, b, h)
-                        # 32 query rows per wave, or per pair of waves (key split)
-                        assert bq in (32 * waves, 16 * waves) and bk % 32 == 0
-                        # two or three K/V tile buffers each, per key half
-                        assert lds in (4 * bk * 2 * d, 6 * bk * 2 * d, 8 * bk * 2 * d)
-                        assert lds <= 64 * 1024
+                        # 32 query rows per wave, or per two or four waves (key split)
+                        assert bq in (32 * waves, 16 * waves, 8 * waves) and bk % 32 == 0
+                        # two or three K/V tile buffers each, per key part
+                        assert lds in (4 * bk * 2 * d, 6 * bk * 2 * d, 8 * bk * 2 * d,
+                                       16 * bk * 2 * d)
+                        # above 64 KiB only the four-way key split (one workgroup per CU)
+                        assert lds <= 64 * 1024 or (bq == 8 * waves and lds <= 160 * 1024)
                         assert _tile(d, causal, "fp16acc", n, b, h) == _tile(d, causal, "opt", n, b, h)
 
 
@@ -140,7 +142,10 @@ def test_tile_config_rows():
     assert _tile(128, True, "opt", 2049) == (256, 32, 8, 49152)
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
     # two waves on each 32 rows)
-    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 4, 65536)
+    assert _tile(64, True, "opt", 900, 2, 8) == (64, 64, 4, 65536)
+    # at most 256 query blocks of 64 rows and at least 16 key tiles: four waves per 32 rows
+    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 8, 131072)
+    assert _tile(128, False, "opt", 1500, 1, 2) == (64, 32, 8, 131072)
     assert _tile(64, False, "opt", 256, 1, 4) == (64, 64, 4, 65536)
     assert _tile(128, False, "opt", 16384, 1, 3) == (64, 32, 4, 65536)
     assert _tile(128, True, "opt", 16384, 1, 3) == (64, 32, 4, 65536)

@@ -31,6 +31,8 @@ OPT_ROWS = {
     (128, False, rows.SMALL128), (128, True, rows.SMALL128),
     (128, False, rows.SIMPLE128X4), (128, True, rows.SIMPLE128X4),
     (128, False, rows.PP128), (128, True, rows.PP128),
+    (64, False, rows.TINY64), (64, True, rows.TINY64),
+    (128, False, rows.TINY128), (128, True, rows.TINY128),
 }
 
 

@@ -168,7 +168,9 @@ def test_baseline_variant_is_never_routed():
 TAIL_SHAPES = [
     # (B, H, N, d, causal, variant)
     (1, 3, 1000, 64, False, "opt"), (2, 3, 777, 64, True, "opt"),          # small grid, d=64
+    (1, 3, 700, 64, False, "opt"), (2, 3, 1001, 64, True, "opt"),          # (two/four-way)
     (1, 2, 1500, 128, False, "opt"), (1, 2, 1499, 128, True, "opt"),       # small grid, d=128
+    (1, 2, 450, 128, False, "opt"), (1, 2, 449, 128, True, "opt"),         # (four/two-way)
     (4, 16, 1001, 64, False, "opt"), (4, 16, 999, 64, True, "opt"),        # simple 8 waves
     (1, 32, 2501, 64, False, "opt"),                                        # simple, d=64
     (1, 8, 8000, 64, False, "opt"), (1, 8, 8500, 64, True, "opt"),         # ping-pong d=64

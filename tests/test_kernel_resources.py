@@ -19,7 +19,7 @@ import pytest
 RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" / "fa" / \
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
-SIMPLE, KSPLIT, PINGPONG16 = 0, 3, 4
+SIMPLE, KSPLIT, PINGPONG16, KSPLIT4 = 0, 3, 4, 5
 
 
 def _load():
@@ -44,7 +44,7 @@ def _min_occupancy(name: str) -> int:
     if family == "flash_fwd_pingpong16":
         return 2                      # waves w and w+4 share a SIMD
     if family == "flash_fwd_ksplit":
-        return 2                      # 64 KiB of LDS: two 4-wave workgroups per CU
+        return 2                      # two 4-wave workgroups (64 KiB) or one 8-wave (128 KiB)
     assert family == "flash_fwd_kernel" and sched == SIMPLE, name
     return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
 
@@ -64,4 +64,6 @@ def test_kernels_keep_their_occupancy():
     for name, r in _load().items():
         want = _min_occupancy(name)
         assert r["occupancy"] >= want, (name, r, want)
-        assert r["lds"] <= 64 * 1024, (name, r)
+        four_way = (_family(name) == "flash_fwd_ksplit"
+                    and int(TILE.search(name).group(5)) == KSPLIT4)
+        assert r["lds"] <= (160 if four_way else 64) * 1024, (name, r)

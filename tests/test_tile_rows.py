@@ -47,13 +47,19 @@ SIMPLE64X8 = (256, 64, 8, 32768)
 SIMPLE128X4 = (128, 32, 4, 32768)
 SMALL64 = (64, 64, 4, 65536)     # key split: 64 rows, 2 x 2 waves, BC=64
 SMALL128 = (64, 32, 4, 65536)    # key split: 64 rows, 2 x 2 waves, BC=32
+TINY64 = (64, 64, 8, 131072)     # four-way key split: 64 rows, 4 x 2 waves, BC=64
+TINY128 = (64, 32, 8, 131072)    # four-way key split: 64 rows, 4 x 2 waves, BC=32
 
 ROWS = [
     # (B, H, N, d, causal, expected tile)
-    (1, 3, 1000, 64, False, SMALL64),
-    (2, 8, 1000, 64, True, SMALL64),          # the benchmark's ragged config
-    (1, 2, 1500, 128, False, SMALL128),
-    (1, 2, 1500, 128, True, SMALL128),
+    (1, 3, 900, 64, False, SMALL64),          # 15 key tiles: two-way split
+    (2, 8, 900, 64, True, SMALL64),
+    (1, 3, 1000, 64, False, TINY64),          # 48 query blocks of 64, 16 key tiles
+    (2, 8, 1000, 64, True, TINY64),           # the benchmark's ragged config
+    (1, 12, 1500, 128, False, SMALL128),      # 288 query blocks of 64: two-way split
+    (1, 12, 1500, 128, True, SMALL128),
+    (1, 2, 1500, 128, False, TINY128),
+    (1, 2, 1500, 128, True, TINY128),
     (4, 16, 1000, 64, False, SIMPLE64X8),
     (1, 32, 2500, 64, False, SIMPLE64X8),
     (4, 16, 1000, 64, True, SIMPLE64X8),
@@ -79,6 +85,11 @@ SWITCHES = [
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
     (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, SIMPLE64X8),
+    # four-way split: at most 256 query blocks of 64 rows and at least 16 key tiles
+    (1, 16, 1024, 64, False, TINY64), (1, 17, 1024, 64, False, SMALL64),
+    (1, 16, 960, 64, True, SMALL64), (1, 16, 961, 64, True, TINY64),
+    (1, 16, 1024, 128, True, TINY128), (1, 17, 1024, 128, True, SMALL128),
+    (1, 16, 480, 128, False, SMALL128), (1, 16, 481, 128, False, TINY128),
     # d=64 ping-pong from 4096 keys (causal 8192)
     (1, 16, 4095, 64, False, SIMPLE64X8), (1, 16, 4096, 64, False, PP64),
     (1, 16, 8191, 64, True, SIMPLE64X8), (1, 16, 8192, 64, True, PP64),
