@@ -136,6 +136,44 @@ def test_overflow_recompute(d, causal):
     _close(o_split, ref)
 
 
+@pytest.mark.parametrize("n, causal", [(8192, False), (8192, True), (6000, True)])
+def test_overflow_at_many_points(n, causal):
+    """Keys from a per-head position on are scaled x8 (scores rising by ~30 exp2 units against
+    the first tile's max): the unchecked run of the d=128 ping-pong overflows at a different key
+    in every head -- in the first chunk, at later chunk boundaries of its early exit, in the last
+    chunk, or only in the checked band or last tile -- and each such item leaves its first pass
+    at a boundary or fails its final test, then runs checked. 1x16x8192 causal runs (long,
+    short) pairs, where a pair whose first item needed the second pass runs its second item
+    checked at once; 1x16x6000 causal runs single blocks (one with a wave past the end). Every
+    row of every head against the fp32 oracle."""
+    from fa import native
+
+    b, h, d = 1, 16, 128
+    t = native.tile_config(d, causal, "opt", n, b, h)
+    assert (t["block_q"], t["waves"]) == (256, 8), t
+    import ctypes
+    from pathlib import Path
+
+    geo = ctypes.CDLL(str(Path(__file__).resolve().parent / "geometry" / "libfa_geom.so"))
+    geo.geom_causal_pairs_pay.argtypes = [ctypes.c_longlong, ctypes.c_int, ctypes.c_int]
+    if causal:
+        assert geo.geom_causal_pairs_pay(b * h, -(-n // 256), 256) == (1 if n == 8192 else 0)
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(b, h, n, d, generator=g)
+    k = torch.randn(b, h, n, d, generator=g)
+    v = torch.randn(b, h, n, d, generator=g)
+    # onset of the large keys per head: first tiles, early and late chunks, band, never
+    onsets = [40, 100, 200, 400, 700, 1000, 1500, 2200, 3000, 4000, 5000, 6000, 7000,
+              n - 300, n - 40, n]
+    for hi, p in enumerate(onsets):
+        k[:, hi, p:] *= 8.0
+    q, k, v = q.half(), k.half(), v.half()
+    print(f"case overflow points B={b} H={h} N={n} causal={causal}", flush=True)
+    out = _fa().forward(q.cuda(), k.cuda(), v.cuda(), causal=causal)
+    assert torch.isfinite(out).all()
+    _close(out, orc.attention_fp32(q, k, v, causal=causal))
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_wide_score_spread(causal):
     """q, k ~ N(0, 1.9^2): scores of standard deviation about 5 in exp2 units, whose row maxima
