@@ -140,6 +140,18 @@ constexpr int tr16_col(int lane) { return 4 * (lane & 3); }
 // query is always lane % 32 of the wave's 32 queries.
 constexpr int st_key(int lane, int nb, int r) { return 32 * nb + mfma32_c_row(lane, r); }
 
+// st_key splits into a lane part and a compile-time accumulator part:
+// st_key(lane, nb, r) = st_key(0, nb, r) + st_key_lane(lane).
+constexpr int st_key_lane(int lane) { return 4 * (lane >> 5); }
+
+// Masking of a score tile: key kt + st_key(lane, nb, r) is masked iff it is >= n or (causal)
+// right of the lane's query qrow, i.e. iff it exceeds min(n - 1, qrow). With the split above,
+// that is st_key(0, nb, r) > st_mask_limit(n, kt, qrow, lane, causal): one threshold per lane and
+// tile, then one compare and one select per score.
+constexpr int st_mask_limit(int n, int kt, int qrow, int lane, bool causal) {
+    return (causal && qrow < n - 1 ? qrow : n - 1) - kt - st_key_lane(lane);
+}
+
 // Key offset (within a 16-key MFMA step) of operand slot i (0..7) of the P.V product. Equal to
 // the score accumulator that feeds it: slot i of step h is accumulator 8*h + i of its block.
 constexpr int pv_key(int lane, int i) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }

@@ -209,17 +209,15 @@ __device__ __forceinline__ void qk_tile(const char* kl, const Frag<T>& fr,
     }
 }
 
-// Keys >= n, and (causal) keys right of the lane's query, get -inf.
+// Keys >= n, and (causal) keys right of the lane's query, get -inf: one lane threshold, then a
+// compare against each accumulator's compile-time key offset and a select per score.
 template <class T, bool CAUSAL>
 __device__ __forceinline__ void mask_tile(f32x16 (&s)[T::NB], int kt, int n, int qrow, int lane) {
+    const int lim = g::st_mask_limit(n, kt, qrow, lane, CAUSAL);
 #pragma unroll
     for (int nb = 0; nb < T::NB; ++nb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kt + g::st_key(lane, nb, r);
-            const bool masked = key >= n || (CAUSAL && key > qrow);
-            s[nb][r] = masked ? -INFINITY : s[nb][r];
-        }
+        for (int r = 0; r < 16; ++r) s[nb][r] = g::st_key(0, nb, r) > lim ? -INFINITY : s[nb][r];
 }
 
 // Online softmax of one tile in base 2 (csrc/kernels/flash_fwd.cu:347-422 is the reference's).
@@ -303,20 +301,23 @@ __device__ __forceinline__ void softmax_optimistic(const f32x16 (&s)[T::NB], flo
 
 // Softmax of one tile for the simple and key-split schedules: optimistic first when the tile
 // is LAZY (FA_OPTIMISTIC), exact (softmax_tile, with the rescale of O) when that overflows or
-// the tile is not LAZY.
-template <class T>
+// the tile is not LAZY. FIRST marks the first tile of the item, which the callers peel off
+// their loops: its running max is -inf, so the optimistic pass would always overflow, and O is
+// still zero, so it needs no rescale; both are left out there. (A run-time flag instead costs
+// the d=128 causal simple tile 68 VGPRs and a third of its occupancy.)
+template <class T, bool FIRST>
 __device__ __forceinline__ void softmax_any(const f32x16 (&s)[T::NB], float scale_log2,
                                             float& m_run, float& l_run, f32x16 (&oacc)[T::DB],
                                             f16x8 (&p)[T::NB][2]) {
     bool exact = true;
-    if constexpr (T::LAZY && FA_OPTIMISTIC) {
+    if constexpr (T::LAZY && FA_OPTIMISTIC && !FIRST) {
         softmax_optimistic<T>(s, scale_log2, m_run, l_run, exact, p);
     }
     if (exact) {
         float alpha;
         bool rescale;
         softmax_tile<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
-        if (rescale) rescale_o<T>(oacc, alpha);
+        if (!FIRST && rescale) rescale_o<T>(oacc, alpha);
     }
 }
 
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     // Tile j in buffer B: its DMA landed (with three buffers the next tile's may still be in
     // flight: its 2 * DMA_ITERS requests are the newest), barrier, refill of the buffer read by
     // the previous tile with tile j + NBUF - 1, then S = QK^T, mask, softmax and O += PV.
-    auto tile = [&](int j, auto b) {
+    auto tile = [&](int j, auto b, auto first) {
         constexpr int B = decltype(b)::value;
         using Refill = std::integral_constant<int, (B + NBUF - 1) % NBUF>;
         if (NBUF == 3 && j > j_begin && j + 1 < n_tiles) {
@@ -508,24 +509,27 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
         qk_tile<T>(kbuf(b), fr, qf, s);
         if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
-        softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
+        softmax_any<T, decltype(first)::value>(s, scale_log2, m_run, l_run, oacc, p);
         pv_tile<T>(vbuf(b), fr, p, oacc);
     };
-    int j = j_begin;
+    // The item has at least one tile (an empty split returned above); the first is peeled off.
+    using Later = std::false_type;
+    tile(j_begin, I0{}, std::true_type{});
+    int j = j_begin + 1;
     if constexpr (NBUF == 3) {
         for (; j + 3 <= n_tiles; j += 3) {
-            tile(j, I0{});
-            tile(j + 1, I1{});
-            tile(j + 2, I2{});
+            tile(j, I1{}, Later{});
+            tile(j + 1, I2{}, Later{});
+            tile(j + 2, I0{}, Later{});
         }
-        if (j < n_tiles) tile(j, I0{});
-        if (j + 1 < n_tiles) tile(j + 1, I1{});
+        if (j < n_tiles) tile(j, I1{}, Later{});
+        if (j + 1 < n_tiles) tile(j + 1, I2{}, Later{});
     } else {
         for (; j + 2 <= n_tiles; j += 2) {
-            tile(j, I0{});
-            tile(j + 1, I1{});
+            tile(j, I1{}, Later{});
+            tile(j + 1, I0{}, Later{});
         }
-        if (j < n_tiles) tile(j, I0{});
+        if (j < n_tiles) tile(j, I1{}, Later{});
     }
     if constexpr (SPLIT) {
         const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
@@ -687,7 +691,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     float l_run = 0.0F;
 
     // Step j in buffer B = j % 2: key part H's tile KS j + H.
-    auto step = [&](int j, auto hc, auto b) {
+    auto step = [&](int j, auto hc, auto b, auto first) {
         constexpr int H = decltype(hc)::value;
         using Other = std::integral_constant<int, 1 - decltype(b)::value>;
         wait_vmem();
@@ -704,17 +708,20 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
         qk_tile<T>(kbuf(hc, b), fr, qf, s);
         if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask_tile<T, CAUSAL>(s, kt, n, qrow, lane);
         f16x8 p[T::NB][2];
-        softmax_any<T>(s, scale_log2, m_run, l_run, oacc, p);
+        softmax_any<T, decltype(first)::value>(s, scale_log2, m_run, l_run, oacc, p);
         pv_tile<T>(vbuf(hc, b), fr, p, oacc);
     };
-    // wave-uniform branch; every part passes the same number of barriers
+    // wave-uniform branch; every part passes the same number of barriers. n_steps >= 1; step 0
+    // (each part's first tile) is peeled off.
     with_part([&](auto hc) {
-        int j = 0;
+        using Later = std::false_type;
+        step(0, hc, I0{}, std::true_type{});
+        int j = 1;
         for (; j + 2 <= n_steps; j += 2) {
-            step(j, hc, I0{});
-            step(j + 1, hc, I1{});
+            step(j, hc, I1{}, Later{});
+            step(j + 1, hc, I0{}, Later{});
         }
-        if (j < n_steps) step(j, hc, I0{});
+        if (j < n_steps) step(j, hc, I1{}, Later{});
     });
 
     // Merge. In round d (d = KS/2, ..., 1), part p + d (p < d) writes (m, l) to its buffer k_0

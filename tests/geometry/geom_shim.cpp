@@ -17,6 +17,10 @@ int geom_mfma16_c_col(int lane) { return g::mfma16_c_col(lane); }
 int geom_tr16_row(int lane) { return g::tr16_row(lane); }
 int geom_tr16_col(int lane) { return g::tr16_col(lane); }
 int geom_st_key(int lane, int nb, int r) { return g::st_key(lane, nb, r); }
+int geom_st_key_lane(int lane) { return g::st_key_lane(lane); }
+int geom_st_mask_limit(int n, int kt, int qrow, int lane, int causal) {
+    return g::st_mask_limit(n, kt, qrow, lane, causal != 0);
+}
 int geom_m16_key(int kb, int i) { return g::m16_key(kb, i); }
 int geom_m16_kchunk(int dc, int grp, int d) { return g::m16_kchunk(dc, grp, d); }
 int geom_m16_kslot_row(int slot, int d) { return g::m16_kslot_row(slot, d); }

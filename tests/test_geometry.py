@@ -384,6 +384,54 @@ def test_mask_predicates(geo, causal):
                     bool(causal) and allm_causal)
 
 
+def test_st_key_splits_into_lane_and_accumulator_parts(geo):
+    for lane, nb, r in itertools.product(range(64), range(4), range(16)):
+        assert geo.geom_st_key(lane, nb, r) == geo.geom_st_key(0, nb, r) + geo.geom_st_key_lane(lane)
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_score_mask_threshold(geo, causal):
+    """The simple and key-split tiles mask accumulator (nb, r) of `lane` iff
+    st_key(0, nb, r) > st_mask_limit(...): that must be exactly "key >= n, or (causal) key right
+    of the lane's query" for every lane, accumulator, tile and query of a tile that is masked."""
+    k0 = {(nb, r): geo.geom_st_key(0, nb, r) for nb in range(2) for r in range(16)}
+    lane_key = {(lane, nb, r): geo.geom_st_key(lane, nb, r)
+                for lane in range(64) for nb in range(2) for r in range(16)}
+    for n, bk in itertools.product([1, 31, 64, 65, 100, 200], [32, 64]):
+        for qw in range(0, n + 32, 32):
+            for kt in range(0, n + bk, bk):
+                for lane in range(64):
+                    qrow = qw + (lane & 31)
+                    lim = geo.geom_st_mask_limit(n, kt, qrow, lane, causal)
+                    for nb in range(bk // 32):
+                        for r in range(16):
+                            key = kt + lane_key[(lane, nb, r)]
+                            want = key >= n or (causal and key > qrow)
+                            assert (k0[(nb, r)] > lim) == want, (n, bk, qw, kt, lane, nb, r)
+
+
+def test_score_mask_threshold_catches_a_dropped_bound(geo):
+    """Planted on the CPU: a threshold that forgets n (causal rows past the end) or the query
+    must disagree with the direct predicate somewhere."""
+    def lim_without_n(n, kt, qrow, lane):
+        return qrow - kt - geo.geom_st_key_lane(lane)
+
+    def lim_without_q(n, kt, qrow, lane):
+        return n - 1 - kt - geo.geom_st_key_lane(lane)
+
+    for bad in (lim_without_n, lim_without_q):
+        found = False
+        for n, kt, lane, nb, r in itertools.product([40, 100], [0, 32, 64], range(64), range(2),
+                                                   range(16)):
+            qrow = 64 + (lane & 31)
+            key = kt + geo.geom_st_key(lane, nb, r)
+            want = key >= n or key > qrow
+            if (geo.geom_st_key(0, nb, r) > bad(n, kt, qrow, lane)) != want:
+                found = True
+                break
+        assert found, bad.__name__
+
+
 @pytest.mark.parametrize("causal", [0, 1])
 def test_work_map_is_a_bijection(geo, causal):
     for bhc, nqb in [(1, 1), (6, 9), (16, 128), (512, 16)]:
