@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -49,6 +50,14 @@
 // Workspace of fa_flash_fwd_splitkv_static (see static_scratch below): FA_STATIC_SCRATCH_BYTES
 // (fa_hip.h) per GPU.
 static __device__ __align__(256) float scratch[FA_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+// Overflow record of the ping-pong's unchecked softmax, per GPU: the id of a launch (high 32
+// bits; every launch gets a new one, never 0) and the number of its workgroups that had to redo
+// an item with the checked softmax (low 32). A workgroup of the same launch that starts after
+// FA_PP16_ADAPT_WGS of them runs its items checked from the start. Best effort: workgroups of
+// the first round start before any overflow is known, and counts of launches that run at once
+// on other streams can be dropped.
+static __device__ unsigned long long pp_overflow_record;
 
 namespace fa {
 namespace {
@@ -429,7 +438,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
-    float* __restrict__ lse_part) {
+    float* __restrict__ lse_part, unsigned /*launch_id*/) {
     // One LDS object per buffer, and the buffer of each tile fixed at compile time (the loop is
     // unrolled by the buffer count): the compiler then sees that the refill of one buffer cannot
     // alias the reads of another and waits for a tile's DMA only at the barrier that starts the
@@ -619,7 +628,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
-    float* /*lse_part*/) {
+    float* /*lse_part*/, unsigned /*launch_id*/) {
     constexpr int KS = T::KS;
     static_assert(KS == 2 || KS == 4, "two or four key parts");
     // One LDS object per (key part, buffer) for K and V, and the buffer of each step fixed at
@@ -925,6 +934,31 @@ using PP16ReadSched = std::conditional_t<
 #ifndef FA_PP16_EXIT_STEPS
 #define FA_PP16_EXIT_STEPS 32
 #endif
+// A ping-pong workgroup runs its items checked from the start once this many workgroups of the
+// same launch have had to redo an item (pp_overflow_record); 0 never does.
+#ifndef FA_PP16_ADAPT_WGS
+#define FA_PP16_ADAPT_WGS 8
+#endif
+
+// Counts one more workgroup of launch `id` in pp_overflow_record that had to redo an item (one
+// lane). The first count of a launch claims the record with one compare-and-swap; every other
+// count is an atomic add, which cannot fail however many workgroups count at once (a retry loop
+// of compare-and-swaps let about one of them through per round). If another launch holds the
+// record (launches on other streams), the count is dropped: the switch is best effort.
+__device__ __forceinline__ void note_overflow(unsigned id) {
+    unsigned long long cur =
+        __hip_atomic_load(&pp_overflow_record, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (static_cast<unsigned>(cur >> 32) != id) {
+        if (__hip_atomic_compare_exchange_strong(
+                &pp_overflow_record, &cur, (static_cast<unsigned long long>(id) << 32) | 1ULL,
+                __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            return;
+        }
+        if (static_cast<unsigned>(cur >> 32) != id) return;  // (cur: the value found)
+    }
+    __hip_atomic_fetch_add(&pp_overflow_record, 1ULL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Unchecked softmax (non-causal ping-pong): the matrix phase adds the row sums of P after MFMA
 // pairs FA_PP16_SUM_PAIR, +2, ... (pair 8 measured best of 1, 4, 8, 10, 12, 13; one v_dot2
 // after each pair from 6, 8 or 10 instead lost 1-3 %). FA_PP16_UNCHECKED 0 keeps the per-tile
@@ -1396,7 +1430,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
-    float* __restrict__ lse_part) {
+    float* __restrict__ lse_part, unsigned launch_id) {
     static_assert((T::D == 128 && T::BC == 32) || (T::D == 64 && T::BC == 64),
                   "the 16x16x32 layouts are written for D=128, BC=32 and D=64, BC=64");
     using G = M16<T>;
@@ -1417,6 +1451,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     // registers rather than threadIdx or __syncthreads_or, which would keep the work-item ids
     // live across the item loop (past 256 VGPRs, into scratch).
     __shared__ int pp_flags[3];
+    // An item's first pass runs checked from the start (1) after enough overflows in this
+    // launch: wave 0 reads pp_overflow_record with the item's prologue loads and writes the
+    // decision here before the prologue's barrier, so that every wave takes the same one.
+    constexpr bool ADAPT = UNCHECKED && FA_PP16_ADAPT_WGS > 0;
+    __shared__ int pp_adapt;
     __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
     __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
@@ -1495,6 +1534,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     load_tile<T>(kh, 2 * T::BC, nk_load, kbuf(I2{}), dma_k);
     load_tile<T>(vh, T::BC, nk_load, vbuf(I1{}), dma);
     load_q16<T>(q + head, qw, n, lane, negate_q, qf);
+    // (after the prologue's loads: its address comes through a scalar load and wait)
+    unsigned long long record = 0;
+    if constexpr (ADAPT) {
+        if (!checked_pass && wave == 0) {
+            record = __hip_atomic_load(&pp_overflow_record, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     const Frag16<T> fr(lane);
 
     f32x4 oacc[G::DB][G::QB];
@@ -1505,7 +1552,18 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     float l_run[G::QB] = {0.0F, 0.0F};
 
     wait_vmem();
+    if constexpr (ADAPT) {
+        if (!checked_pass && wave == 0 && lane == 0) {
+            pp_adapt = static_cast<unsigned>(record >> 32) == launch_id &&
+                               static_cast<unsigned>(record) >= FA_PP16_ADAPT_WGS
+                           ? 1
+                           : 0;
+        }
+    }
     __syncthreads();
+    // (workgroup-uniform: one LDS word written before the barrier)
+    const bool start_checked =
+        ADAPT && !checked_pass && __builtin_amdgcn_readfirstlane(pp_adapt) != 0;
 #pragma unroll
     for (int qb = 0; qb < G::QB; ++qb)
 #pragma unroll
@@ -1646,9 +1704,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             // must mask (keys 0..q0 are visible to every row), i.e. the diagonal band. The
             // second pass runs every steady tile checked.
             const int n_free =
-                checked_pass ? 0
-                             : (CAUSAL ? min(n_busy, max(0, min(q0 - key0 + 1, nk)) / T::BC)
-                                       : n_busy);
+                (checked_pass || start_checked)
+                    ? 0
+                    : (CAUSAL ? min(n_busy, max(0, min(q0 - key0 + 1, nk)) / T::BC) : n_busy);
             int slot = 0;
             int chunk = 1;  // steps
             while (jj + 3 <= n_free) {
@@ -1705,6 +1763,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     if (n_steady > 0) {
         const bool aborted = grp == 0 ? steady(I0{}) : steady(I1{});
         if (aborted) {
+            if constexpr (ADAPT) {
+                if (wave == 0 && lane == 0) note_overflow(launch_id);
+            }
             // the DMA still in flight lands before the second pass refills the buffers
             wait_vmem();
             __syncthreads();
@@ -1738,7 +1799,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
             if (wave_any(bad) && lane == 0) flags[2] = 1;
             __syncthreads();
-            if (__builtin_amdgcn_readfirstlane(flags[2]) != 0) return false;
+            if (__builtin_amdgcn_readfirstlane(flags[2]) != 0) {
+                if constexpr (ADAPT) {
+                    if (wave == 0 && lane == 0) note_overflow(launch_id);
+                }
+                return false;
+            }
         }
     }
     if constexpr (SPLIT) {
@@ -2019,6 +2085,16 @@ Scale scale_of(float softmax_scale) {
     return r;
 }
 
+// Id of a kernel launch, for pp_overflow_record: process-wide, never 0. (A launch captured in a
+// HIP graph keeps its id in every replay, so replays after one whose items overflowed may start
+// their items checked: the same results, at the checked softmax's speed.)
+unsigned next_launch_id() {
+    static std::atomic<unsigned> seq{0};
+    unsigned id = seq.fetch_add(1, std::memory_order_relaxed) + 1;
+    if (id == 0) id = seq.fetch_add(1, std::memory_order_relaxed) + 1;
+    return id;
+}
+
 // One launch of kernel T (SPLIT: the split-KV partial pass over n_splits * items workgroups).
 template <class T, bool CAUSAL, bool SPLIT = false>
 int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_splits = 1,
@@ -2033,8 +2109,9 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
     int nqb = n_qblocks;
     float scale_log2 = sc.log2e_scaled;
     int negate_q = sc.negate_q;
+    unsigned launch_id = next_launch_id();
     void* args[] = {&qp, &kp, &vp, &op, &lse, &n, &bh, &nqb, &scale_log2, &negate_q,
-                    &tiles_per_split, &o_part, &lse_part};
+                    &tiles_per_split, &o_part, &lse_part, &launch_id};
     dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh) *
               static_cast<unsigned>(n_splits));
     const void* fn;

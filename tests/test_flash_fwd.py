@@ -191,6 +191,28 @@ def test_wide_score_spread(causal):
         _close(out.view(b * h, n, d)[bh, rows], ref)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_overflows_switch_later_workgroups_to_checked(causal):
+    """Inputs on which most ping-pong items overflow fp16 against their first tile's max (q, k ~
+    N(0, 1.9^2)) on a grid of several rounds (4x16x4096 d=128: 1024 workgroups, or 512 causal
+    pairs, on 256 CUs): once a few workgroups of a launch have redone an item, the ones that
+    start later run their items checked from the start (pp_overflow_record, keyed by the
+    launch). Every slice against the fp32 oracle, for two launches in a row, then a launch on
+    N(0, 1) inputs of the same shape, which must not inherit the switch's state (a new launch
+    id) and is checked the same way."""
+    b, h, n, d = 4, 16, 4096, 128
+    q, k, v = _qkv(b, h, n, d, seed=15)
+    q, k = q * 1.9, k * 1.9
+    ref = orc.attention_fp32(q.cpu(), k.cpu(), v.cpu(), causal=causal)
+    for rep in range(2):
+        print(f"case spread switch B={b} H={h} N={n} causal={causal} launch {rep}", flush=True)
+        _close(_fa().forward(q, k, v, causal=causal), ref)
+    q2, k2, v2 = _qkv(b, h, n, d, seed=16)
+    print(f"case plain after spread B={b} H={h} N={n} causal={causal}", flush=True)
+    _close(_fa().forward(q2, k2, v2, causal=causal),
+           orc.attention_fp32(q2.cpu(), k2.cpu(), v2.cpu(), causal=causal))
+
+
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_sink(d, causal):
