@@ -69,6 +69,9 @@ namespace g = fa::geom;
 
 // Compile-time tile shape and options. Counterpart of the reference's Config/Opt pair
 // (csrc/kernels/flash_fwd.cu:70-100), re-derived for 64-wide waves and 32x32 MFMA blocks.
+// FA_OPTIMISTIC 1: the simple and key-split tiles with lazy rescale first take p against the
+// running max, without the tile's row max, and fall back to the exact softmax of the tile only
+// if some p overflows fp16 (softmax_any); 0: the exact softmax in every tile.
 #ifndef FA_OPTIMISTIC
 #define FA_OPTIMISTIC 1
 #endif
