@@ -943,6 +943,17 @@ using PP16ReadSched = std::conditional_t<
 #define FA_PP16_ADAPT_WGS 8
 #endif
 
+// Flags that the waves of a workgroup share in LDS, ordered by the workgroup's barriers. Relaxed
+// workgroup-scope atomics compile to ds_read / ds_write, which wait for LDS alone; volatile
+// accesses compile to flat instructions (a volatile access keeps its generic address), which
+// also count as vector-memory operations, so each waited for every K/V prefetch in flight.
+__device__ __forceinline__ int flag_get(const int& f) {
+    return __hip_atomic_load(&f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void flag_set(int& f, int v) {
+    __hip_atomic_store(&f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Counts one more workgroup of launch `id` in pp_overflow_record that had to redo an item (one
 // lane). The first count of a launch claims the record with one compare-and-swap; every other
 // count is an atomic add, which cannot fail however many workgroups count at once (a retry loop
@@ -1452,7 +1463,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     // Overflow flags of the unchecked run (0-1, one per chunk mod 2) and of the item's final
     // test (2). Cleared at the start of an item's first pass; read with the lane and wave
     // registers rather than threadIdx or __syncthreads_or, which would keep the work-item ids
-    // live across the item loop (past 256 VGPRs, into scratch).
+    // live across the item loop (past 256 VGPRs, into scratch). Accessed with flag_get and
+    // flag_set (LDS instructions).
     __shared__ int pp_flags[3];
     // An item's first pass runs checked from the start (1) after enough overflows in this
     // launch: wave 0 reads pp_overflow_record with the item's prologue loads and writes the
@@ -1529,7 +1541,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     if constexpr (FAST) {
         // cleared before the prologue's barrier; the previous pass or item read them before
         // its own final barrier
-        if (!checked_pass && wave == 0 && lane < 3) static_cast<volatile int*>(pp_flags)[lane] = 0;
+        if (!checked_pass && wave == 0 && lane < 3) flag_set(pp_flags[lane], 0);
     }
     load_tile<T>(kh, 0, nk_load, kbuf(I0{}), dma_k);
     load_tile<T>(vh, 0, nk_load, vbuf(I0{}), dma);
@@ -1695,7 +1707,6 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             // most two chunks after the first overflow. The read waits at once (an LDS latency
             // per chunk); the inner loop stays the plain three-tile body, whose timing is
             // sensitive to any extra live value.
-            volatile int* flags = pp_flags;
             // The exit needs every wave in the run. A causal wave that starts past the end of the
             // sequence has no active tile and spends the run in the idle-tile loop below, never
             // reading the flags, so a workgroup with such a wave (only a last query block) keeps
@@ -1714,12 +1725,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             int chunk = 1;  // steps
             while (jj + 3 <= n_free) {
                 // (nothing can be set at the first boundary)
-                if (jj > 1 && __builtin_amdgcn_readfirstlane(flags[slot ^ 1]) != 0) {
+                if (jj > 1 && __builtin_amdgcn_readfirstlane(flag_get(pp_flags[slot ^ 1])) != 0) {
                     aborted = true;
                     break;
                 }
                 const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
-                if (exit_ok && wave_any(bad) && lane == 0) flags[slot] = 1;
+                if (exit_ok && wave_any(bad) && lane == 0) flag_set(pp_flags[slot], 1);
                 const int chunk_end =
                     FA_PP16_EXIT_STEPS > 0 ? min(n_free, jj + 3 * chunk) : n_free;
                 for (; jj + 3 <= chunk_end; jj += 3) {
@@ -1798,11 +1809,10 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         // The flag is cleared again only by the next item, after the barrier between a pair's
         // items.
         if (!checked_pass) {
-            volatile int* flags = pp_flags;
             const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
-            if (wave_any(bad) && lane == 0) flags[2] = 1;
+            if (wave_any(bad) && lane == 0) flag_set(pp_flags[2], 1);
             __syncthreads();
-            if (__builtin_amdgcn_readfirstlane(flags[2]) != 0) {
+            if (__builtin_amdgcn_readfirstlane(flag_get(pp_flags[2])) != 0) {
                 if constexpr (ADAPT) {
                     if (wave == 0 && lane == 0) note_overflow(launch_id);
                 }
@@ -1860,7 +1870,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 continue;
             }
             if (second || pw.qb_short < 0) break;
-            __syncthreads();  // the first item's last LDS reads, before the second item's DMA
+            // the first item's last LDS reads, before the second item's DMA (a barrier that
+            // waits for LDS only: __syncthreads would also wait for the first item's O stores)
+            end_phase<false>();
             second = true;
             checked_pass = redone;
         }
