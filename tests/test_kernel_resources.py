@@ -61,6 +61,10 @@ def test_no_kernel_spills_to_scratch():
 
 
 def test_kernels_keep_their_occupancy():
+    """Occupancy, and at most 64 KiB of LDS per workgroup (the four-way key split aside): on
+    gfx950 K/V tiles placed above the first 64 KiB of a workgroup's LDS measured 2.9 % slower on
+    the causal pair kernels (an unused 64 KiB array declared before them; placed after them, the
+    same 112 KiB cost nothing)."""
     for name, r in _load().items():
         want = _min_occupancy(name)
         assert r["occupancy"] >= want, (name, r, want)
