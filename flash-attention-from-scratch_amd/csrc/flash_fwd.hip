@@ -1854,11 +1854,11 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             const g::Work w = g::work_of(static_cast<int>(blockIdx.x), bh_count, n_qblocks, true);
             pw = g::PairWork{w.bh, w.qb, -1};
         }
-        // One call site of the item code for both items and both passes. (Running the short
-        // block first, in every pair or in every other one, measured the same or up to 1.3 %
-        // slower.) The two items of a
+        // One call site of the item code for both items and both passes. The two items of a
         // pair are query blocks of one head, the second seeing a prefix of the first's keys: if
-        // the first needed the checked pass, the second runs it at once.
+        // the first needed the checked pass, the second runs it at once. (Running the short
+        // block first, in every pair or in every other one, measured the same or up to 1.3 %
+        // slower.)
         bool second = false;
         bool checked_pass = false;
         bool redone = false;
