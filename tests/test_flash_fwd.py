@@ -215,6 +215,27 @@ def test_overflows_switch_later_workgroups_to_checked(causal):
 
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("causal", [False, True])
+def test_very_long_ragged_sequence(d, causal):
+    """Four times the headline length, not a multiple of any tile: 2 heads of 65636 keys (the
+    ping-pong rows; 2000-odd key tiles per item at d=128, so the unchecked run passes its
+    32-step chunk cap many times, and causal pairs whose two items differ a hundredfold; the
+    last query block holds 100 rows). fp64 rows at the start, around the block edges, in the
+    middle and at the end of both heads, then the split-KV launch of the same inputs."""
+    b, h, n = 1, 2, 65536 + 100
+    print(f"case very long B={b} H={h} N={n} d={d} causal={causal}", flush=True)
+    q, k, v = _qkv(b, h, n, d, seed=50 + d)
+    out = _fa().forward(q, k, v, causal=causal).float().cpu()
+    assert torch.isfinite(out).all()
+    o_split = _fa().forward_splitkv(q, k, v, causal=causal)[0].float().cpu()
+    rows = [0, 1, 255, 256, 32767, 32768, n - 101, n - 100, n - 2, n - 1]
+    for bh in range(b * h):
+        ref = torch.from_numpy(orc.attention_fp64_rows(q, k, v, causal, bh, rows)).float()
+        _close(out.view(b * h, n, d)[bh, rows], ref)
+        _close(o_split.view(b * h, n, d)[bh, rows], ref)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("causal", [False, True])
 def test_attention_sink(d, causal):
     """Key 0 about 13 nats above every other key for every query (an attention sink), 16 heads
     of 16384 keys: the ping-pong rows take p against the first key tile's max, which here is
