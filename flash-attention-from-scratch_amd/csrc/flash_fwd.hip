@@ -59,6 +59,23 @@ static __device__ __align__(256) float scratch[FA_STATIC_SCRATCH_BYTES / sizeof(
 // on other streams can be dropped.
 static __device__ unsigned long long pp_overflow_record;
 
+// Timeline probe, a development build option (off in the library): with FA_PROBE 1 wave 0 of
+// every ping-pong workgroup writes the 100 MHz constant clock (s_memrealtime) at fixed points
+// of its items, and its CU and XCC ids, into probe_stamps[blockIdx.x * 16 + slot];
+// fa_probe_clear / fa_probe_read (exported only by such a build) hand the array to the host
+// (dev/fa_dev --probe, summarized by dev/probe.py). Slots: 0 kernel entry; per item i (0, 1),
+// 1 + 5i its first pass starts, 2 + 5i the prologue's loads have landed (after its barrier),
+// 3 + 5i the steady tiles are done, 4 + 5i the last tile is done, 5 + 5i the O stores are
+// issued; 12 a second pass starts; 14 HW_ID; 15 XCC_ID.
+#ifndef FA_PROBE
+#define FA_PROBE 0
+#endif
+#if FA_PROBE
+constexpr int kProbeSlots = 16;
+constexpr unsigned kProbeWorkgroups = 1U << 16;
+static __device__ unsigned long long probe_stamps[kProbeWorkgroups * kProbeSlots];
+#endif
+
 namespace fa {
 namespace {
 
@@ -954,6 +971,38 @@ __device__ __forceinline__ void flag_set(int& f, int v) {
     __hip_atomic_store(&f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// FA_PROBE stamps (no code otherwise): the clock at `slot`, and the hardware ids.
+__device__ __forceinline__ void probe_stamp(int wave, int lane, int slot) {
+#if FA_PROBE
+    // The clock is read by every wave (a uniform value) and fed to an empty volatile asm, which
+    // the compiler keeps in order with the kernel's own volatile asm (its s_waitcnt waits), so
+    // the read cannot sink below the next wait.
+    const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+    asm volatile("" ::"s"(t));
+    if (wave == 0 && lane == 0 && blockIdx.x < kProbeWorkgroups) {
+        probe_stamps[blockIdx.x * kProbeSlots + slot] = t;
+    }
+#else
+    (void)wave;
+    (void)lane;
+    (void)slot;
+#endif
+}
+__device__ __forceinline__ void probe_ids(int wave, int lane) {
+#if FA_PROBE
+    // s_getreg operand: register id | offset << 6 | (bits - 1) << 11 (HW_ID 4, XCC_ID 20)
+    constexpr int kHwId = 4 | (0 << 6) | (31 << 11);
+    constexpr int kXccId = 20 | (0 << 6) | (31 << 11);
+    if (wave == 0 && lane == 0 && blockIdx.x < kProbeWorkgroups) {
+        probe_stamps[blockIdx.x * kProbeSlots + 14] = __builtin_amdgcn_s_getreg(kHwId);
+        probe_stamps[blockIdx.x * kProbeSlots + 15] = __builtin_amdgcn_s_getreg(kXccId);
+    }
+#else
+    (void)wave;
+    (void)lane;
+#endif
+}
+
 // Counts one more workgroup of launch `id` in pp_overflow_record that had to redo an item (one
 // lane). The first count of a launch claims the record with one compare-and-swap; every other
 // count is an atomic add, which cannot fail however many workgroups count at once (a retry loop
@@ -1481,6 +1530,9 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int lane = threadIdx.x & 63;
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int grp = wave >> 2;
+    probe_stamp(wave, lane, 0);
+    probe_ids(wave, lane);
+    int probe_item = 0;  // (FA_PROBE only) items this workgroup has finished
     const int items = bh_count * n_qblocks;
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
     // One (head, query block) item: the whole single-item kernel. With UNCHECKED, a first pass
@@ -1489,6 +1541,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     // softmax in every steady tile, which redoes an overflowing tile with a rescale, and always
     // stores.
     auto run_item = [&](const g::Work w, const bool checked_pass) -> bool {
+    probe_stamp(wave, lane, checked_pass ? 12 : 1 + 5 * probe_item);
     constexpr bool FAST = UNCHECKED;
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const int q0 = w.qb * T::BR;
@@ -1576,6 +1629,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         }
     }
     __syncthreads();
+    probe_stamp(wave, lane, 2 + 5 * probe_item);
     // (workgroup-uniform: one LDS word written before the barrier)
     const bool start_checked =
         ADAPT && !checked_pass && __builtin_amdgcn_readfirstlane(pp_adapt) != 0;
@@ -1786,6 +1840,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             return false;
         }
     }
+    probe_stamp(wave, lane, 3 + 5 * probe_item);
     char* kb[3];
     char* vb[3];
     kb[0] = k_lds0;
@@ -1803,6 +1858,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         general_tiles16<T, CAUSAL>(n_steady, n_tiles, n_act, nk, qk, lane, kh, vh, kb, vb, dma_k,
                                    dma, fr_g, qf, s, oacc, scale_log2, m_run, l_run);
     }
+    probe_stamp(wave, lane, 4 + 5 * probe_item);
     if constexpr (FAST) {
         // an overflowing p makes its row sum infinite (NaN inputs make it NaN): decided for the
         // whole workgroup (flag 2 after a barrier), whose waves then redo the item together.
@@ -1832,6 +1888,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
                    m_run, l_run, oacc);
     }
+    probe_stamp(wave, lane, 5 + 5 * probe_item);
+    ++probe_item;
     return true;
     };
     // With UNCHECKED: a second pass of the same code, every steady tile checked, when some p
@@ -2606,3 +2664,17 @@ int fa_flash_fwd_splitkv_static(const fa_params* params, float* lse, int32_t num
 }
 
 }  // extern "C"
+
+#if FA_PROBE
+// Development build only (FA_PROBE 1): the ping-pong's timeline stamps of the current device.
+extern "C" __attribute__((visibility("default"))) int fa_probe_clear(void) {
+    static unsigned long long zeros[kProbeWorkgroups * kProbeSlots];
+    return hipMemcpyToSymbol(HIP_SYMBOL(probe_stamps), zeros, sizeof(zeros), 0,
+                             hipMemcpyHostToDevice) == hipSuccess ? 0 : 1;
+}
+extern "C" __attribute__((visibility("default"))) int fa_probe_read(void* dst, uint64_t bytes) {
+    const uint64_t size = sizeof(unsigned long long) * kProbeWorkgroups * kProbeSlots;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(probe_stamps), bytes < size ? bytes : size, 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : 1;
+}
+#endif

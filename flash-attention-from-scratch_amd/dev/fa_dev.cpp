@@ -1,7 +1,7 @@
 // fa_dev -- standalone driver of the attention forward, without Python or PyTorch.
 //
 //   fa_dev [B H N D causal iters variant] [--lib PATH] [--warmup-ms MS] [--seed S] [--json]
-//          [--std X] [--boost-keys FRAC:FACTOR] [--sink NATS] [--splitkv S]
+//          [--std X] [--boost-keys FRAC:FACTOR] [--sink NATS] [--splitkv S] [--probe PATH]
 //          defaults:  4 8 4096 128 0 20 opt,  --lib <this dir>/../fa/libfa_hip.so
 //   variant: base | baseline | opt | fp16acc
 //   --std X                 inputs ~ N(0, X^2) instead of N(0, 1)
@@ -15,6 +15,10 @@
 //   --splitkv S             run the split-KV entry point (fa_flash_fwd_splitkv) with S key
 //                           ranges per query block (0 = the library's automatic plan) and a
 //                           workspace of the plan's size; the timing covers both launches
+//   --probe PATH            (a library built with FA_PROBE=1, e.g. dev/ab.py build probe
+//                           --define FA_PROBE=1) after the timed launches, one more launch
+//                           with the ping-pong's timeline stamps cleared before it; writes
+//                           them to PATH (16 uint64 per workgroup; dev/probe.py reads them)
 //
 // Loads the kernel library at run time (dlopen) and calls only its C ABI (include/fa_hip.h),
 // as any foreign caller would: that lets the tuning sweep (dev/tune.py) time libraries built
@@ -161,6 +165,7 @@ struct Options {
     float boost = 1.0F;
     float sink = 0.0F;  // 0: no sink
     int splitkv = -1;  // < 0: fa_flash_fwd; else fa_flash_fwd_splitkv with this many ranges
+    std::string probe;  // "": no timeline dump
 };
 
 Options parse(int argc, char** argv) {
@@ -188,6 +193,8 @@ Options parse(int argc, char** argv) {
             o.std = std::stof(value());
         } else if (s == "--sink") {
             o.sink = std::stof(value());
+        } else if (s == "--probe") {
+            o.probe = value();
         } else if (s == "--boost-keys") {
             const std::string v = value();
             const auto colon = v.find(':');
@@ -376,6 +383,36 @@ int run(const Options& o) {
     }
     if (!ok) std::printf("FAILED: |err| above 2e-3 + 1e-2 |ref| on a sampled row\n");
 
+    if (!o.probe.empty()) {
+        // The stamps of one more launch (workgroups [0, 65536), 16 slots each), written up to
+        // the last workgroup that stamped.
+        void* h = dlopen(o.lib.c_str(), RTLD_NOW | RTLD_LOCAL | RTLD_NOLOAD);
+        auto* clear = h ? reinterpret_cast<int (*)()>(dlsym(h, "fa_probe_clear")) : nullptr;
+        auto* read = h ? reinterpret_cast<int (*)(void*, uint64_t)>(dlsym(h, "fa_probe_read"))
+                       : nullptr;
+        if (clear == nullptr || read == nullptr) {
+            throw std::runtime_error("--probe needs a library built with FA_PROBE=1");
+        }
+        hip_check(hipStreamSynchronize(stream), "probe: drain");
+        if (clear() != 0) throw std::runtime_error("fa_probe_clear failed");
+        launch();
+        hip_check(hipStreamSynchronize(stream), "probe launch");
+        std::vector<uint64_t> stamps(size_t{1} << 20);
+        if (read(stamps.data(), stamps.size() * sizeof(uint64_t)) != 0) {
+            throw std::runtime_error("fa_probe_read failed");
+        }
+        size_t used = 0;
+        for (size_t i = 0; i < stamps.size(); ++i) {
+            if (stamps[i] != 0) used = i / 16 + 1;
+        }
+        FILE* f = std::fopen(o.probe.c_str(), "wb");
+        if (f == nullptr) throw std::runtime_error("cannot write " + o.probe);
+        const size_t wrote = std::fwrite(stamps.data(), sizeof(uint64_t), used * 16, f);
+        std::fclose(f);
+        if (wrote != used * 16) throw std::runtime_error("short write to " + o.probe);
+        std::printf("probe: %zu workgroups -> %s\n", used, o.probe.c_str());
+    }
+
     hip_check(hipEventDestroy(e0), "hipEventDestroy");
     hip_check(hipEventDestroy(e1), "hipEventDestroy");
     hip_check(hipStreamDestroy(stream), "hipStreamDestroy");
@@ -393,7 +430,7 @@ int main(int argc, char** argv) {
         std::fprintf(stderr,
                      "error: %s\nusage: fa_dev [B H N D causal iters variant] [--lib PATH] "
                      "[--warmup-ms MS] [--seed S] [--json] [--std X] [--boost-keys FRAC:FAC] [--sink NATS] "
-                     "[--splitkv S]\n",
+                     "[--splitkv S] [--probe PATH]\n",
                      e.what());
         return 2;
     } catch (const std::exception& e) {

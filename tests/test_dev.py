@@ -111,3 +111,76 @@ def test_fa_dev_runs_and_checks(args):
     assert res.returncode == 0, res.stdout + res.stderr
     rec = json.loads(res.stdout.splitlines()[0])
     assert rec["check"] == "ok" and rec["max_abs_err"] < 2e-2 and rec["tflops"] > 0
+
+
+def _stamps(wgs):
+    """A synthetic timeline dump: per workgroup (cu, xcc, entry, [item phase lengths in
+    ticks]) -> 16 uint64 slots as the FA_PROBE build writes them."""
+    import numpy as np
+
+    out = np.zeros((len(wgs), 16), dtype=np.uint64)
+    for w, (cu, xcc, entry, items) in enumerate(wgs):
+        out[w, 0] = entry
+        t = entry
+        for i, (lead, *phases) in enumerate(items):
+            t += lead
+            out[w, 1 + 5 * i] = t
+            for k, dt in enumerate(phases):
+                t += dt
+                out[w, 2 + 5 * i + k] = t
+        out[w, 14] = cu << 8
+        out[w, 15] = xcc
+    return out
+
+
+def test_probe_summary_of_synthetic_stamps(tmp_path):
+    """dev/probe.py on a dump whose phases are known: two CUs of XCD 0 and one of XCD 1, two
+    workgroups in turn on each CU, 150 ticks (1.5 us) apart; phases of 300, 10000, 100, 150
+    ticks after an entry-to-item lead of 10."""
+    sys.path.insert(0, str(DEV))
+    import probe
+
+    item = [(10, 300, 10000, 100, 150)]
+    span = 10 + 300 + 10000 + 100 + 150
+    wgs = []
+    for cu, xcc, skew in [(0, 0, 0), (1, 0, 50), (0, 1, 400)]:
+        wgs.append((cu, xcc, 1000 + skew, item))
+        wgs.append((cu, xcc, 1000 + skew + span + 150, item))
+    path = tmp_path / "stamps.bin"
+    _stamps(wgs).tofile(path)
+    s = probe.summarize(probe.load(path))
+    assert (s["workgroups"], s["cus"], s["pairs"], s["second_passes"]) == (6, 3, False, 0)
+    approx = pytest.approx
+    assert s["items"][0] == approx({"prologue": 3.0, "steady": 100.0, "last_tile": 1.0,
+                                    "final_and_store": 1.5})
+    assert s["entry_to_item"] == approx(0.1)
+    assert s["gap_between_workgroups_on_a_cu"] == approx(1.5)
+    end = (2 * span + 150) / 100.0
+    assert s["cu_end"] == approx({"min": end, "median": end + 0.5, "max": end + 4.0})
+    assert s["xcd_end"] == approx([end + 0.5, end + 4.0])
+    assert "launch" in probe.report(s)
+
+
+def test_probe_summary_of_pairs(tmp_path):
+    """A causal pair workgroup: the second item's phases and the gap between the items."""
+    sys.path.insert(0, str(DEV))
+    import probe
+
+    path = tmp_path / "pairs.bin"
+    _stamps([(0, 0, 500, [(10, 300, 20000, 40, 200), (120, 280, 5000, 30, 190)])]).tofile(path)
+    s = probe.summarize(probe.load(path))
+    assert s["pairs"] and s["gap_between_items"] == pytest.approx(1.2)
+    assert s["items"][1] == pytest.approx({"prologue": 2.8, "steady": 50.0, "last_tile": 0.3,
+                                           "final_and_store": 1.9})
+
+
+def test_library_has_no_probe_symbols():
+    """The timeline probe is a development build (FA_PROBE=1): the library as built exports
+    neither of its functions, and its kernels hold no stamp array."""
+    import ctypes
+
+    lib = REPO / "flash-attention-from-scratch_amd" / "fa" / "libfa_hip.so"
+    if not lib.exists():
+        pytest.skip("library not built")
+    so = ctypes.CDLL(str(lib))
+    assert not hasattr(so, "fa_probe_read") and not hasattr(so, "fa_probe_clear")
