@@ -66,7 +66,8 @@ static __device__ unsigned long long pp_overflow_record;
 // (dev/fa_dev --probe, summarized by dev/probe.py). Slots: 0 kernel entry; per item i (0, 1),
 // 1 + 5i its first pass starts, 2 + 5i the prologue's loads have landed (after its barrier),
 // 3 + 5i the steady tiles are done, 4 + 5i the last tile is done, 5 + 5i the O stores are
-// issued; 12 a second pass starts; 14 HW_ID; 15 XCC_ID.
+// issued; 12 a second pass starts; 11 and 13 the shader clock's cycle count (s_memtime) at the
+// workgroup's entry and end; 14 HW_ID; 15 XCC_ID.
 #ifndef FA_PROBE
 #define FA_PROBE 0
 #endif
@@ -988,6 +989,19 @@ __device__ __forceinline__ void probe_stamp(int wave, int lane, int slot) {
     (void)slot;
 #endif
 }
+// The shader clock's cycle count at `slot` (with the clock stamps, the workgroup's mean clock).
+__device__ __forceinline__ void probe_cycles(int wave, int lane, int slot) {
+#if FA_PROBE
+    // (at the workgroup's entry and end only: nothing to keep in order around it)
+    if (wave == 0 && lane == 0 && blockIdx.x < kProbeWorkgroups) {
+        probe_stamps[blockIdx.x * kProbeSlots + slot] = __builtin_amdgcn_s_memtime();
+    }
+#else
+    (void)wave;
+    (void)lane;
+    (void)slot;
+#endif
+}
 __device__ __forceinline__ void probe_ids(int wave, int lane) {
 #if FA_PROBE
     // s_getreg operand: register id | offset << 6 | (bits - 1) << 11 (HW_ID 4, XCC_ID 20)
@@ -1531,6 +1545,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int grp = wave >> 2;
     probe_stamp(wave, lane, 0);
+    probe_cycles(wave, lane, 11);
     probe_ids(wave, lane);
     int probe_item = 0;  // (FA_PROBE only) items this workgroup has finished
     const int items = bh_count * n_qblocks;
@@ -1939,6 +1954,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                                n_qblocks, CAUSAL)
                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
     }
+    probe_cycles(wave, lane, 13);
 }
 
 // ---- tile table -------------------------------------------------------------------------------

@@ -6,10 +6,12 @@ Per workgroup the dump holds 16 uint64 values: the 100 MHz constant clock (s_mem
 slot 0 (kernel entry) and, for item i of the workgroup (0, or 1 for the second item of a causal
 pair), slots 1 + 5i .. 5 + 5i (its first pass starts, its prologue's loads have landed, its
 steady tiles are done, its last tile is done, its O stores are issued); slot 12 when a second
-pass starts; the HW_ID (14) and XCC_ID (15) hardware registers. Printed: medians over the
+pass starts; slots 11 and 13 the shader clock's cycle count (s_memtime) at the workgroup's
+entry and end; the HW_ID (14) and XCC_ID (15) hardware registers. Printed: medians over the
 workgroups of each phase of each item and of the gap between a pair's items; the idle time
 between one workgroup's last stamp and the next workgroup's entry on the same CU; when the
-CUs and the XCDs finish, from the first workgroup's entry. Only the stamps of wave 0 are
+CUs and the XCDs finish, from the first workgroup's entry; and each XCD's median clock (cycles
+over 100 MHz ticks from entry to the last O store). Only the stamps of wave 0 are
 recorded, so the phases are that wave's view (the barriers make them the workgroup's).
 """
 
@@ -76,6 +78,13 @@ def summarize(a: np.ndarray) -> dict:
         cu_end.append(ends[order].max())
     xcc = a[:, 15] & 0xF
     xcd_end = [float(ends[xcc == x].max()) for x in np.unique(xcc)]
+    last = np.where(a[:, 10] != 0, a[:, 10], a[:, 5])
+    have = (a[:, 11] != 0) & (a[:, 13] != 0) & (last > a[:, 0])
+    if have.any():
+        ns = (last - a[:, 0]) * (1000.0 / TICKS_PER_US)
+        ghz = (a[:, 13] - a[:, 11]) / np.where(ns > 0, ns, 1.0)  # cycles per ns
+        out["xcd_clock_ghz"] = [float(np.median(ghz[have & (xcc == x)]))
+                                for x in np.unique(xcc)]
     out["cus"] = int(len(cu_end))
     out["gap_between_workgroups_on_a_cu"] = float(np.median(gaps)) if gaps else None
     out["cu_end"] = {"min": float(np.min(cu_end)), "median": float(np.median(cu_end)),
@@ -101,6 +110,9 @@ def report(s: dict) -> str:
     lines.append(f"CUs finish at {c['min']:.1f} / {c['median']:.1f} / {c['max']:.1f} us "
                  f"(min / median / max)")
     lines.append("XCDs finish at " + ", ".join(f"{x:.1f}" for x in s["xcd_end"]) + " us")
+    if "xcd_clock_ghz" in s:
+        lines.append("XCD clocks (median over their workgroups) "
+                     + ", ".join(f"{x:.3f}" for x in s["xcd_clock_ghz"]) + " GHz")
     return "\n".join(lines)
 
 

@@ -184,3 +184,21 @@ def test_library_has_no_probe_symbols():
         pytest.skip("library not built")
     so = ctypes.CDLL(str(lib))
     assert not hasattr(so, "fa_probe_read") and not hasattr(so, "fa_probe_clear")
+
+
+def test_probe_xcd_clocks(tmp_path):
+    """The XCD clock from the shader cycle counts (slots 11 and 13) over the 100 MHz stamps:
+    a workgroup of XCD 0 that runs 10,000 ticks (100 us) and 200,000 cycles is at 2.0 GHz, one
+    of XCD 1 with 190,000 cycles at 1.9 GHz."""
+    sys.path.insert(0, str(DEV))
+    import probe
+
+    item = [(10, 300, 9440, 100, 150)]  # 10,000 ticks from entry to the O stores
+    a = _stamps([(0, 0, 1000, item), (0, 1, 1000, item)])
+    a[0, 11], a[0, 13] = 5_000, 205_000
+    a[1, 11], a[1, 13] = 7_000, 197_000
+    path = tmp_path / "clocks.bin"
+    a.tofile(path)
+    s = probe.summarize(probe.load(path))
+    assert s["xcd_clock_ghz"] == pytest.approx([2.0, 1.9])
+    assert "GHz" in probe.report(s)
