@@ -120,6 +120,19 @@ constexpr int m16_kslot_chunk(int slot, int d) {
 constexpr int st16_key(int lane, int kb, int r) { return m16_key(kb, mfma16_c_row(lane, r)); }
 constexpr int st16_query(int lane, int qb) { return 16 * qb + (lane & 15); }
 
+// st16_key splits into a lane part and a compile-time accumulator part, as st_key does:
+// st16_key(lane, kb, r) = st16_key(0, kb, r) + st16_key_lane(lane) (lane / 16 = 2h + a selects
+// the 8-row half a and the 16-row half h of the key block).
+constexpr int st16_key_lane(int lane) { return 4 * ((lane >> 4) & 1) + 16 * (lane >> 5); }
+
+// Mask threshold of query block qb of a 16x16 score tile (as st_mask_limit): key
+// kt + st16_key(lane, kb, r) is masked for query qw + st16_query(lane, qb) iff it is >= n or
+// (causal) right of that query, i.e. iff st16_key(0, kb, r) > st16_mask_limit(...).
+constexpr int st16_mask_limit(int n, int kt, int qw, int lane, int qb, bool causal) {
+    const int qrow = qw + st16_query(lane, qb);
+    return (causal && qrow < n - 1 ? qrow : n - 1) - kt - st16_key_lane(lane);
+}
+
 // Key carried by operand slot i (0..7) of k step t (32 keys) of the O^T += V^T P^T MFMA in
 // `lane`: slots 0..3 are the lane's scores of key block 2t, slots 4..7 those of block 2t + 1,
 // so P^T of query block qb is the lane's own 8 exponentials in order (no shuffle), and the

@@ -102,12 +102,19 @@ namespace g = fa::geom;
 #endif
 
 // Main-loop schedules: SIMPLE (flash_fwd_kernel: each wave runs QK, softmax and PV of a tile in
-// turn), KSPLIT / KSPLIT4 (flash_fwd_ksplit: two or four waves per 32 query rows, each on every
-// second or fourth key tile),
-// PINGPONG16 (flash_fwd_pingpong16: two groups of waves alternate between an MFMA-only phase and
-// a softmax phase, on 16x16x32 MFMAs; the table's long d = 128 rows). The values are those the
-// -D tile overrides name.
-enum Sched { SIMPLE = 0, KSPLIT = 3, PINGPONG16 = 4, KSPLIT4 = 5 };
+// turn, on 32x32x16 MFMAs), SIMPLE16 (flash_fwd_simple16: the same schedule with the ping-pong's
+// 16x16x32 tile math), KSPLIT / KSPLIT4 (flash_fwd_ksplit: two or four waves per 32 query rows,
+// each on every second or fourth key tile), PINGPONG16 (flash_fwd_pingpong16: two groups of
+// waves alternate between an MFMA-only phase and a softmax phase, on 16x16x32 MFMAs; the table's
+// long d = 128 rows). The values are fa_tile_info's `schedule` (fa_schedule) and the names the
+// -D tile overrides use.
+enum Sched {
+    SIMPLE = FA_SCHED_SIMPLE,
+    KSPLIT = FA_SCHED_KSPLIT,
+    PINGPONG16 = FA_SCHED_PINGPONG16,
+    KSPLIT4 = FA_SCHED_KSPLIT4,
+    SIMPLE16 = FA_SCHED_SIMPLE16
+};
 
 // K/V buffers of the simple schedule: 2 (refill one tile ahead, wait for all DMA at each tile)
 // or 3 (two tiles ahead; a tile waits only for its own DMA, the next tile's stays in flight).
@@ -140,10 +147,12 @@ struct Tile {
     static constexpr int ROW_BYTES = 2 * D;
     static constexpr int CPR = D / 8;                  // 16-byte chunks per row
     static constexpr int TILE_BYTES = BC * ROW_BYTES;  // one K or V tile
-    static constexpr bool M16 = SCHED == PINGPONG16;      // 16x16x32 layouts
+    static constexpr bool M16 = SCHED == PINGPONG16 || SCHED == SIMPLE16;  // 16x16x32 layouts
     static constexpr int NBUF =  // per K, V (the simple schedule's third only within 64 KiB)
         SCHED == PINGPONG16 ? 3
-                            : (SCHED == SIMPLE && 6 * TILE_BYTES <= 64 * 1024 ? FA_SIMPLE_NBUF : 2);
+                            : ((SCHED == SIMPLE || SCHED == SIMPLE16) && 6 * TILE_BYTES <= 64 * 1024
+                                   ? FA_SIMPLE_NBUF
+                                   : 2);
     static constexpr int LDS_BYTES = 2 * NBUF * TILE_BYTES * KS;
     static constexpr int NB = BC / 32;                 // 32-key MFMA blocks per tile
     static constexpr int KK = D / 16;                  // 16-deep MFMA steps over D
@@ -1957,21 +1966,311 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     probe_cycles(wave, lane, 13);
 }
 
+// ---- kernel, simple schedule on 16x16x32 MFMAs ------------------------------------------------
+// S^T = K Q^T of one tile with each K fragment read right before its MFMAs (8 VGPRs of K live at
+// a time instead of the 32 that qk16 reads ahead): the simple schedule runs four waves per SIMD
+// and so has 128 VGPRs per wave.
+template <class T>
+__device__ __forceinline__ void qk16_lean(const char* kl, const Frag16<T>& fr,
+                                          const f16x8 (&qf)[M16<T>::QB][M16<T>::DC],
+                                          f32x4 (&s)[M16<T>::KB][M16<T>::QB]) {
+    using G = M16<T>;
+#pragma unroll
+    for (int kb = 0; kb < G::KB; ++kb) {
+        f16x8 kf[G::DC];
+#pragma unroll
+        for (int dc = 0; dc < G::DC; ++dc)
+            kf[dc] = *reinterpret_cast<const f16x8*>(kl + fr.koff[kb][dc]);
+#pragma unroll
+        for (int qb = 0; qb < G::QB; ++qb) {
+            s[kb][qb] = f32x4{};
+#pragma unroll
+            for (int dc = 0; dc < G::DC; ++dc) s[kb][qb] = mfma16(kf[dc], qf[qb][dc], s[kb][qb]);
+        }
+    }
+}
+
+// O^T += V^T P^T of one tile, V^T fragments of one 32-key step read right before its MFMAs.
+template <class T>
+__device__ __forceinline__ void pv16_lean(const char* vl, const Frag16<T>& fr,
+                                          const f16x8 (&p)[M16<T>::QB][M16<T>::KS],
+                                          f32x4 (&oacc)[M16<T>::DB][M16<T>::QB]) {
+    using G = M16<T>;
+#pragma unroll
+    for (int t = 0; t < G::KS; ++t) {
+        f16x8 vf[G::DB];
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+            const char* base = vl + fr.voff[db] + 32 * t * G::ROW;
+            const f16x4 lo = lds_read_tr16(base);
+            const f16x4 up = lds_read_tr16(base + 8 * G::ROW);
+            vf[db] = f16x8{lo[0], lo[1], lo[2], lo[3], up[0], up[1], up[2], up[3]};
+        }
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+            for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = mfma16(vf[db], p[qb][t], oacc[db][qb]);
+    }
+}
+
+// Optimistic softmax of one tile (as softmax16_optimistic) with each group of 8 exponentials
+// (one P^T operand) packed and summed at once: 8 temporaries live instead of 32.
+template <class T>
+__device__ __forceinline__ void softmax16_optimistic_lean(
+    const f32x4 (&s)[M16<T>::KB][M16<T>::QB], float scale_log2, const float (&m_run)[M16<T>::QB],
+    float (&l_run)[M16<T>::QB], bool& overflow, f16x8 (&p)[M16<T>::QB][M16<T>::KS]) {
+    using G = M16<T>;
+    float sum[G::QB] = {0.0F, 0.0F};
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+        for (int t = 0; t < G::KS; ++t) {
+            float e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                e[i] = exp2_fast(fmaf(s[2 * t + (i >> 2)][qb][i & 3], scale_log2, -m_run[qb]));
+            p[qb][t] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+            sum[qb] = sum8_f16(p[qb][t], sum[qb]);
+        }
+    overflow = wave_any(!(sum[0] < INFINITY && sum[1] < INFINITY));
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) l_run[qb] = overflow ? l_run[qb] : l_run[qb] + sum[qb];
+}
+
+// Exact online softmax of one tile (as softmax16_tile with its row sums), each group of 8
+// exponentials packed and summed at once.
+template <class T>
+__device__ __forceinline__ void softmax16_tile_lean(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
+                                                    float scale_log2, float (&m_run)[M16<T>::QB],
+                                                    float (&l_run)[M16<T>::QB],
+                                                    float (&alpha)[M16<T>::QB], bool& rescale,
+                                                    f16x8 (&p)[M16<T>::QB][M16<T>::KS]) {
+    using G = M16<T>;
+    float mx[G::QB];
+    bool grow = false;
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) {
+        float x = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x = fmaxf(x, s[kb][qb][r]);
+        mx[qb] = max_xor32(max_xor16(x)) * scale_log2;
+        grow = grow || (T::LAZY ? (mx[qb] > m_run[qb] + 8.0F) : (mx[qb] > m_run[qb]));
+    }
+    rescale = wave_any(grow);
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) {
+        const float m_new = rescale ? fmaxf(m_run[qb], mx[qb]) : m_run[qb];
+        const float m_use = (m_new == -INFINITY) ? 0.0F : m_new;
+        alpha[qb] = exp2_fast(m_run[qb] - m_use);
+        m_run[qb] = m_new;
+        float sum = 0.0F;
+#pragma unroll
+        for (int t = 0; t < G::KS; ++t) {
+            float e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                e[i] = exp2_fast(fmaf(s[2 * t + (i >> 2)][qb][i & 3], scale_log2, -m_use));
+            p[qb][t] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+            sum = sum8_f16(p[qb][t], sum);
+        }
+        l_run[qb] = (rescale ? l_run[qb] * alpha[qb] : l_run[qb]) + sum;
+    }
+}
+
+// Keys >= n, and (causal) keys right of the query, get -inf (as mask16): one threshold per query
+// block and lane (fa::geom::st16_mask_limit), then a compare and a select per score.
+template <class T, bool CAUSAL>
+__device__ __forceinline__ void mask16_lim(f32x4 (&s)[M16<T>::KB][M16<T>::QB], int kt, int n,
+                                           int qw, int lane) {
+    using G = M16<T>;
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) {
+        const int lim = g::st16_mask_limit(n, kt, qw, lane, qb, CAUSAL);
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                s[kb][qb][r] = g::st16_key(0, kb, r) > lim ? -INFINITY : s[kb][qb][r];
+    }
+}
+
+// Softmax of one tile for flash_fwd_simple16, as softmax_any: optimistic against the running
+// max, exact (with the rescale of O) on an overflow; FIRST (the item's first tile, peeled off the
+// loop) exact without a rescale.
+template <class T, bool FIRST>
+__device__ __forceinline__ void softmax16_any(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
+                                              float scale_log2, float (&m_run)[M16<T>::QB],
+                                              float (&l_run)[M16<T>::QB],
+                                              f32x4 (&oacc)[M16<T>::DB][M16<T>::QB],
+                                              f16x8 (&p)[M16<T>::QB][M16<T>::KS]) {
+    bool exact = true;
+    if constexpr (T::LAZY && FA_OPTIMISTIC && !FIRST) {
+        softmax16_optimistic_lean<T>(s, scale_log2, m_run, l_run, exact, p);
+    }
+    if (exact) {
+        float alpha[M16<T>::QB];
+        bool rescale;
+        softmax16_tile_lean<T>(s, scale_log2, m_run, l_run, alpha, rescale, p);
+        if (!FIRST && rescale) rescale16<T>(oacc, alpha);
+    }
+}
+
+// flash_fwd_kernel's schedule (per tile: barrier, prefetch, then S = QK^T, mask, softmax and
+// O += PV in turn; the item's first tile peeled off) on the ping-pong's 16x16x32 MFMAs and
+// layouts (K tiles in the Frag16 read layout, V tiles with row_xor_m16, P^T straight from the
+// lane's own exponentials). Each wave holds 32 query rows as two 16-row blocks, and each lane
+// 4 keys of 2 queries per 16-key block. Same arguments, grid and results as flash_fwd_kernel.
+template <class T, bool CAUSAL, bool SPLIT = false>
+__global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
+    float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
+    float* __restrict__ lse_part, unsigned /*launch_id*/) {
+    static_assert(T::SCHED == SIMPLE16, "16x16x32 simple schedule");
+    static_assert((T::D == 128 && T::BC == 32) || (T::D == 64 && T::BC == 64),
+                  "the 16x16x32 layouts are written for D=128, BC=32 and D=64, BC=64");
+    using G = M16<T>;
+    constexpr int NBUF = T::NBUF;
+    __shared__ __attribute__((aligned(1024))) char k_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char k_lds2[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds0[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds1[T::TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) char v_lds2[T::TILE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_uniform(threadIdx.x >> 6);
+    const int items = bh_count * n_qblocks;
+    const int split = SPLIT ? static_cast<int>(blockIdx.x) / items : 0;
+    auto run_item = [&](const g::Work w) {
+    const size_t head = static_cast<size_t>(w.bh) * n * T::D;
+    const f16* kh = k + head;
+    const f16* vh = v + head;
+    const int q0 = w.qb * T::BR;
+    const int qw = q0 + wave * 32;  // first query of this wave
+    const int n_all = g::num_kv_tiles(n, q0, T::BR, T::BC, CAUSAL);
+    const g::KeyRange range = SPLIT ? g::split_range(n_all, tiles_per_split, split)
+                                    : g::KeyRange{0, n_all};
+    const int j_begin = range.begin;
+    const int n_tiles = range.begin + range.count;  // absolute: tiles [j_begin, n_tiles)
+    if (SPLIT && range.count == 0) return;           // workgroup-uniform
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    auto kbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? k_lds0 : (B == 1 ? k_lds1 : k_lds2);
+    };
+    auto vbuf = [&](auto b) {
+        constexpr int B = decltype(b)::value;
+        return B == 0 ? v_lds0 : (B == 1 ? v_lds1 : v_lds2);
+    };
+
+    constexpr int PRIO = T::D == 128 ? FA_SIMPLE_PRIO_D128 : FA_SIMPLE_PRIO_D64;
+    const TileDma<T, true> dma_k(wave, lane);  // K tiles in the layout of Frag16's K reads
+    const TileDma<T> dma(wave, lane);          // V tiles, swizzle fa::geom::row_xor_m16
+    load_tile<T>(kh, j_begin * T::BC, n, kbuf(I0{}), dma_k);
+    load_tile<T>(vh, j_begin * T::BC, n, vbuf(I0{}), dma);
+    if constexpr (NBUF == 3) {
+        if (j_begin + 1 < n_tiles) {
+            load_tile<T>(kh, (j_begin + 1) * T::BC, n, kbuf(I1{}), dma_k);
+            load_tile<T>(vh, (j_begin + 1) * T::BC, n, vbuf(I1{}), dma);
+        }
+    }
+    f16x8 qf[G::QB][G::DC];
+    load_q16<T>(q + head, qw, n, lane, negate_q, qf);
+    const Frag16<T> fr(lane);
+
+    f32x4 oacc[G::DB][G::QB];
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < G::QB; ++qb) oacc[db][qb] = f32x4{};
+    float m_run[G::QB] = {-INFINITY, -INFINITY};  // running maxima, log2 domain (scaled)
+    float l_run[G::QB] = {0.0F, 0.0F};            // the lane's partial row sums (its keys)
+
+    // Tile j in buffer B, as in flash_fwd_kernel.
+    auto tile = [&](int j, auto b, auto first) {
+        constexpr int B = decltype(b)::value;
+        using Refill = std::integral_constant<int, (B + NBUF - 1) % NBUF>;
+        if (NBUF == 3 && j > j_begin && j + 1 < n_tiles) {
+            // vmcnt(2 * DMA_ITERS) lgkmcnt(0): only the next tile's requests stay in flight
+            __builtin_amdgcn_s_waitcnt(static_cast<short>(0x0070 | (2 * T::DMA_ITERS)));
+        } else {
+            wait_vmem();
+        }
+        __syncthreads();  // tile j is in LDS for every wave; tile j-1's buffers are free
+        if (j + NBUF - 1 < n_tiles) {
+            load_tile<T>(kh, (j + NBUF - 1) * T::BC, n, kbuf(Refill{}), dma_k);
+            load_tile<T>(vh, (j + NBUF - 1) * T::BC, n, vbuf(Refill{}), dma);
+        }
+        const int kt = j * T::BC;
+        if (qw >= n || g::tile_fully_masked(kt, qw, 32, CAUSAL)) return;  // wave-uniform
+        f32x4 s[G::KB][G::QB];
+        if constexpr (PRIO & 1) __builtin_amdgcn_s_setprio(1);
+        qk16_lean<T>(kbuf(b), fr, qf, s);
+        if constexpr (PRIO & 1) __builtin_amdgcn_s_setprio(0);
+        if (g::tile_needs_mask(n, kt, T::BC, qw, CAUSAL)) mask16_lim<T, CAUSAL>(s, kt, n, qw, lane);
+        f16x8 p[G::QB][G::KS];
+        softmax16_any<T, decltype(first)::value>(s, scale_log2, m_run, l_run, oacc, p);
+        if constexpr (PRIO & 2) __builtin_amdgcn_s_setprio(1);
+        pv16_lean<T>(vbuf(b), fr, p, oacc);
+        if constexpr (PRIO & 2) __builtin_amdgcn_s_setprio(0);
+    };
+    using Later = std::false_type;
+    tile(j_begin, I0{}, std::true_type{});
+    int j = j_begin + 1;
+    if constexpr (NBUF == 3) {
+        for (; j + 3 <= n_tiles; j += 3) {
+            tile(j, I1{}, Later{});
+            tile(j + 1, I2{}, Later{});
+            tile(j + 2, I0{}, Later{});
+        }
+        if (j < n_tiles) tile(j, I1{}, Later{});
+        if (j + 1 < n_tiles) tile(j + 1, I2{}, Later{});
+    } else {
+        // (the odd last tile inside the loop: a second instance of the tile code after it would
+        // keep its own copies of the fragment offsets live across the loop)
+        for (; j < n_tiles; j += 2) {
+            tile(j, I1{}, Later{});
+            if (j + 1 < n_tiles) tile(j + 1, I0{}, Later{});
+        }
+    }
+    if constexpr (SPLIT) {
+        const size_t part = static_cast<size_t>(split) * bh_count + w.bh;
+        store16_partial<T>(o_part + part * n * T::D, lse_part + part * n, qw, n, lane, m_run,
+                           l_run, oacc);
+    } else {
+        store16<T>(o + head, lse ? lse + static_cast<size_t>(w.bh) * n : nullptr, qw, n, lane,
+                   m_run, l_run, oacc);
+    }
+    };
+    run_item(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
+                                n_qblocks, CAUSAL)
+                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
+}
+
 // ---- tile table -------------------------------------------------------------------------------
 // Counterpart of the reference's per-(variant, d, causal) `using` lines
 // (csrc/kernels/flash_fwd.cu:597-612). On MI355X the best tile also depends on the sequence
 // length and the grid size, so the "opt" / "fp16acc" rows are split by N at thresholds found by
-// the tile sweep (FA2-paper shapes, B*N = 16k tokens):
+// the tile sweep (FA2-paper shapes, B*N = 16k tokens, and interleaved A/B of the candidates):
 //   * d = 64: the 8-wave simple schedule (256-row workgroups, 64-key tiles, two workgroups per
-//     CU); from 4096 keys (causal: 8192) the 16x16x32 ping-pong with 64-key tiles, when its
-//     one workgroup per CU fills whole rounds (non-causal: the last round at least 95 % full;
-//     causal: where the launcher runs pairs, fa::geom::causal_pairs_pay). Measured against the
-//     simple tile: non-causal +1.7 / +2.8 / +3.4 % at 4096 / 8192 / 16384 keys (B*N = 64k
-//     tokens, H = 16), causal +1.8 / +4.4 % at 8192 / 16384; with partly empty last rounds
-//     -0.1 % (3x16x6144) to -5.1 % (3x16x6144 causal), and causal -3.0 % at 4096;
+//     CU) on 16x16x32 MFMAs (SIMPLE16); causal up to 2048 keys on 32x32x16 MFMAs (SIMPLE).
+//     SIMPLE16 against SIMPLE: non-causal +1.2 / +3.9 / +4.8 / +3.8 % at 512 / 1024 / 2048 /
+//     4096 keys, causal +1.8 / +2.0 / +3.4 % at 3072 / 4096 (two grids); against the d = 64
+//     ping-pong that the table ran on long sequences: non-causal +2.9 / +2.4 / +0.5 / +1.7 %
+//     (4x16x4096, 2x32x8192, 1x16x16384, 1x32x16384), causal +1.6 / +6.1 / +4.0 / -0.7 %
+//     (2x16x8192, 2x32x8192, 1x32x16384, 1x16x16384). Causal at 1024 and 2048 keys it measured
+//     -1.3 to +0.8 % (and -0.8 to -2.5 % on the many-heads shape with outlier keys);
 //   * d = 128: the 16x16x32 ping-pong for long sequences; below a threshold the 4-wave simple
 //     tile, which has no pipeline prologue and epilogue per workgroup (and, when causal, fewer
-//     diagonal tiles);
+//     diagonal tiles): on 16x16x32 MFMAs above 256 keys (causal 512; +3.3 / +5.2 % at 512 /
+//     768, causal +1.0 / +2.7 / +3.8 % at 1024 / 1536 / 2048), else on 32x32x16 (-1.8 % at 256,
+//     causal -1.2 % at 512 on 16x16x32);
 //   * small grids (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000): the
 //     key-split schedule with 64-row workgroups (two waves per 32 query rows, each on half the
 //     key tiles), so the same grid keeps twice the SIMDs busy.
@@ -2009,37 +2308,43 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #define FA_TINY_MIN_TILES 16
 #endif
 #ifndef FA_OPT_D64
-#define FA_OPT_D64 64, 8, true, SIMPLE
+#define FA_OPT_D64 64, 8, true, SIMPLE16
+#endif
+#ifndef FA_OPT_D64_CAUSAL_SHORT
+#define FA_OPT_D64_CAUSAL_SHORT 64, 8, true, SIMPLE
 #endif
 #ifndef FA_OPT_D64_CAUSAL
-#define FA_OPT_D64_CAUSAL 64, 8, true, SIMPLE
+#define FA_OPT_D64_CAUSAL 64, 8, true, SIMPLE16
 #endif
-#ifndef FA_OPT_D64_LONG
-#define FA_OPT_D64_LONG 64, 8, true, PINGPONG16
+#ifndef FA_D64_CAUSAL_SHORT_MAX_N
+#define FA_D64_CAUSAL_SHORT_MAX_N 2048
 #endif
-#ifndef FA_OPT_D64_CAUSAL_LONG
-#define FA_OPT_D64_CAUSAL_LONG 64, 8, true, PINGPONG16
-#endif
-#ifndef FA_D64_LONG_MIN_N
-#define FA_D64_LONG_MIN_N 4096
-#endif
-#ifndef FA_D64_CAUSAL_LONG_MIN_N
-#define FA_D64_CAUSAL_LONG_MIN_N 8192
+#ifndef FA_OPT_D128_VSHORT
+#define FA_OPT_D128_VSHORT 32, 4, true, SIMPLE
 #endif
 #ifndef FA_OPT_D128_SHORT
-#define FA_OPT_D128_SHORT 32, 4, true, SIMPLE
+#define FA_OPT_D128_SHORT 32, 4, true, SIMPLE16
 #endif
 #ifndef FA_OPT_D128
 #define FA_OPT_D128 32, 8, true, PINGPONG16
 #endif
+#ifndef FA_OPT_D128_CAUSAL_VSHORT
+#define FA_OPT_D128_CAUSAL_VSHORT 32, 4, true, SIMPLE
+#endif
 #ifndef FA_OPT_D128_CAUSAL_SHORT
-#define FA_OPT_D128_CAUSAL_SHORT 32, 4, true, SIMPLE
+#define FA_OPT_D128_CAUSAL_SHORT 32, 4, true, SIMPLE16
 #endif
 #ifndef FA_OPT_D128_CAUSAL
 #define FA_OPT_D128_CAUSAL 32, 8, true, PINGPONG16
 #endif
+#ifndef FA_D128_VSHORT_MAX_N
+#define FA_D128_VSHORT_MAX_N 256
+#endif
 #ifndef FA_D128_SHORT_MAX_N
 #define FA_D128_SHORT_MAX_N 768
+#endif
+#ifndef FA_D128_CAUSAL_VSHORT_MAX_N
+#define FA_D128_CAUSAL_VSHORT_MAX_N 512
 #endif
 #ifndef FA_D128_CAUSAL_SHORT_MAX_N
 #define FA_D128_CAUSAL_SHORT_MAX_N 2048
@@ -2058,8 +2363,8 @@ enum TileId : int {
     BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
     OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
     OPT_D64_TINY, OPT_D64_C_TINY, OPT_D128_TINY, OPT_D128_C_TINY,
-    OPT_D64, OPT_D64_C, OPT_D64_LONG, OPT_D64_C_LONG, OPT_D128_SHORT, OPT_D128, OPT_D128_C_SHORT,
-    OPT_D128_C,
+    OPT_D64, OPT_D64_C_SHORT, OPT_D64_C, OPT_D128_VSHORT, OPT_D128_SHORT, OPT_D128,
+    OPT_D128_C_VSHORT, OPT_D128_C_SHORT, OPT_D128_C,
 };
 template <int ID> struct Row;
 template <> struct Row<BASE_D64> : Entry<Tile<64, FA_BASE_D64>, false> {};
@@ -2075,11 +2380,12 @@ template <> struct Row<OPT_D64_C_TINY> : Entry<Tile<64, FA_OPT_D64_TINY>, true> 
 template <> struct Row<OPT_D128_TINY> : Entry<Tile<128, FA_OPT_D128_TINY>, false> {};
 template <> struct Row<OPT_D128_C_TINY> : Entry<Tile<128, FA_OPT_D128_TINY>, true> {};
 template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
+template <> struct Row<OPT_D64_C_SHORT> : Entry<Tile<64, FA_OPT_D64_CAUSAL_SHORT>, true> {};
 template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
-template <> struct Row<OPT_D64_LONG> : Entry<Tile<64, FA_OPT_D64_LONG>, false> {};
-template <> struct Row<OPT_D64_C_LONG> : Entry<Tile<64, FA_OPT_D64_CAUSAL_LONG>, true> {};
+template <> struct Row<OPT_D128_VSHORT> : Entry<Tile<128, FA_OPT_D128_VSHORT>, false> {};
 template <> struct Row<OPT_D128_SHORT> : Entry<Tile<128, FA_OPT_D128_SHORT>, false> {};
 template <> struct Row<OPT_D128> : Entry<Tile<128, FA_OPT_D128>, false> {};
+template <> struct Row<OPT_D128_C_VSHORT> : Entry<Tile<128, FA_OPT_D128_CAUSAL_VSHORT>, true> {};
 template <> struct Row<OPT_D128_C_SHORT> : Entry<Tile<128, FA_OPT_D128_CAUSAL_SHORT>, true> {};
 template <> struct Row<OPT_D128_C> : Entry<Tile<128, FA_OPT_D128_CAUSAL>, true> {};
 
@@ -2101,18 +2407,14 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
         return causal ? OPT_D128_C_SMALL : OPT_D128_SMALL;
     }
     if (head_dim == 64) {
-        const int64_t nqb = (static_cast<int64_t>(n) + 255) / 256;
-        if (causal) {
-            const bool pp = n >= FA_D64_CAUSAL_LONG_MIN_N &&
-                            g::causal_pairs_pay(bh, static_cast<int>(nqb), g::kCus);
-            return pp ? OPT_D64_C_LONG : OPT_D64_C;
-        }
-        const int64_t items = bh * nqb;
-        const int64_t rounds = (items + g::kCus - 1) / g::kCus;
-        const bool pp = n >= FA_D64_LONG_MIN_N && 100 * items >= 95 * rounds * g::kCus;
-        return pp ? OPT_D64_LONG : OPT_D64;
+        if (!causal) return OPT_D64;
+        return n <= FA_D64_CAUSAL_SHORT_MAX_N ? OPT_D64_C_SHORT : OPT_D64_C;
     }
-    if (!causal) return n <= FA_D128_SHORT_MAX_N ? OPT_D128_SHORT : OPT_D128;
+    if (!causal) {
+        if (n <= FA_D128_VSHORT_MAX_N) return OPT_D128_VSHORT;
+        return n <= FA_D128_SHORT_MAX_N ? OPT_D128_SHORT : OPT_D128;
+    }
+    if (n <= FA_D128_CAUSAL_VSHORT_MAX_N) return OPT_D128_C_VSHORT;
     return n <= FA_D128_CAUSAL_SHORT_MAX_N ? OPT_D128_C_SHORT : OPT_D128_C;
 }
 
@@ -2133,11 +2435,12 @@ decltype(auto) with_row(TileId id, F&& f) {
         case OPT_D128_TINY: return f(Row<OPT_D128_TINY>{});
         case OPT_D128_C_TINY: return f(Row<OPT_D128_C_TINY>{});
         case OPT_D64: return f(Row<OPT_D64>{});
+        case OPT_D64_C_SHORT: return f(Row<OPT_D64_C_SHORT>{});
         case OPT_D64_C: return f(Row<OPT_D64_C>{});
-        case OPT_D64_LONG: return f(Row<OPT_D64_LONG>{});
-        case OPT_D64_C_LONG: return f(Row<OPT_D64_C_LONG>{});
+        case OPT_D128_VSHORT: return f(Row<OPT_D128_VSHORT>{});
         case OPT_D128_SHORT: return f(Row<OPT_D128_SHORT>{});
         case OPT_D128: return f(Row<OPT_D128>{});
+        case OPT_D128_C_VSHORT: return f(Row<OPT_D128_C_VSHORT>{});
         case OPT_D128_C_SHORT: return f(Row<OPT_D128_C_SHORT>{});
         default: return f(Row<OPT_D128_C>{});
     }
@@ -2145,7 +2448,7 @@ decltype(auto) with_row(TileId id, F&& f) {
 
 template <class T>
 constexpr fa_tile_info info_of() {
-    return fa_tile_info{T::BR, T::BC, T::NW * T::KS, T::LDS_BYTES};
+    return fa_tile_info{T::BR, T::BC, T::NW * T::KS, T::LDS_BYTES, T::SCHED};
 }
 
 thread_local std::string g_last_error;
@@ -2205,10 +2508,12 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
               static_cast<unsigned>(n_splits));
     const void* fn;
     if constexpr (SPLIT) {
-        static_assert(T::SCHED == SIMPLE || T::SCHED == PINGPONG16,
-                      "split-KV runs the simple or the 16x16x32 ping-pong schedule");
+        static_assert(T::SCHED == SIMPLE || T::SCHED == SIMPLE16 || T::SCHED == PINGPONG16,
+                      "split-KV runs a simple or the 16x16x32 ping-pong schedule");
         if constexpr (T::SCHED == PINGPONG16) {
             fn = reinterpret_cast<const void*>(&flash_fwd_pingpong16<T, CAUSAL, true>);
+        } else if constexpr (T::SCHED == SIMPLE16) {
+            fn = reinterpret_cast<const void*>(&flash_fwd_simple16<T, CAUSAL, true>);
         } else {
             fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL, true>);
         }
@@ -2222,6 +2527,8 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
         }
     } else if constexpr (T::SCHED == KSPLIT || T::SCHED == KSPLIT4) {
         fn = reinterpret_cast<const void*>(&flash_fwd_ksplit<T, CAUSAL>);
+    } else if constexpr (T::SCHED == SIMPLE16) {
+        fn = reinterpret_cast<const void*>(&flash_fwd_simple16<T, CAUSAL>);
     } else {
         fn = reinterpret_cast<const void*>(&flash_fwd_kernel<T, CAUSAL>);
     }
@@ -2372,11 +2679,11 @@ int64_t tail_heads(const fa_params& p) {
     if (p.variant == FA_VARIANT_BASELINE || p.causal || p.seqlen < FA_SPLITKV_MIN_N) return 0;
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
     const TileId id = tile_id(p.head_dim, false, p.variant, p.seqlen, bh);
-    // the one-workgroup-per-CU rows, and the d = 64 simple row of long sequences, whose first
-    // heads then take the d = 64 ping-pong (whole rounds): d=64 1x9x8192 +36 %, 1x17x8192
-    // +24 %, 1x20x10000 +12 %, 1x36x4096 +10 %, 1x40x5000 +6 % against its single launch
-    const bool d64_long = id == OPT_D64 && p.seqlen >= FA_D64_LONG_MIN_N;
-    if (id != OPT_D128 && id != OPT_D64_LONG && !d64_long) return 0;
+    // the one-workgroup-per-CU rows, and the d = 64 row of long sequences (measured with the
+    // d = 64 ping-pong on the first heads: d=64 1x9x8192 +36 %, 1x17x8192 +24 %, 1x20x10000
+    // +12 %, 1x36x4096 +10 %, 1x40x5000 +6 % against its single launch)
+    const bool d64_long = id == OPT_D64 && p.seqlen >= FA_SPLITKV_MIN_N;
+    if (id != OPT_D128 && !d64_long) return 0;
     if (splitkv_preferred(p)) return 0;
     const int64_t nqb = (static_cast<int64_t>(p.seqlen) + 255) / 256;
     const int64_t items = bh * nqb;

@@ -366,19 +366,19 @@ int run(const Options& o) {
         std::printf(
             "{\"lib\": \"%s\", \"version\": \"%s\", \"variant\": \"%s\", \"B\": %d, \"H\": %d, "
             "\"N\": %d, \"D\": %d, \"causal\": %d, \"block_q\": %d, \"block_k\": %d, "
-            "\"waves\": %d, \"max_abs_err\": %.3e, \"check\": \"%s\", \"iters\": %d, "
+            "\"waves\": %d, \"schedule\": %d, \"max_abs_err\": %.3e, \"check\": \"%s\", \"iters\": %d, "
             "\"median_ms\": %.5f, \"mean_ms\": %.5f, \"min_ms\": %.5f, \"tflops\": %.2f, "
             "\"frac_of_peak\": %.4f, \"splitkv\": %d, \"n_splits\": %d, "
             "\"tiles_per_split\": %d}\n",
             o.lib.c_str(), api.version(), o.variant.c_str(), o.batch, o.heads, o.seqlen,
-            o.head_dim, causal ? 1 : 0, tile.block_q, tile.block_k, tile.waves, max_err,
-            ok ? "ok" : "FAILED", o.iters, median, mean, static_cast<double>(sorted.front()), tf,
+            o.head_dim, causal ? 1 : 0, tile.block_q, tile.block_k, tile.waves, tile.schedule,
+            max_err, ok ? "ok" : "FAILED", o.iters, median, mean, static_cast<double>(sorted.front()), tf,
             tf / kPeakTflops, o.splitkv, plan.num_splits, plan.tiles_per_split);
     } else {
-        std::printf("%s B=%d H=%d N=%d D=%d causal=%d tile=%dx%d/%dw  max_abs_err=%.2e  "
-                    "median=%.4f ms  %.1f TFLOPS (%.1f%% of peak)\n",
+        std::printf("%s B=%d H=%d N=%d D=%d causal=%d tile=%dx%d/%dw sched=%d  "
+                    "max_abs_err=%.2e  median=%.4f ms  %.1f TFLOPS (%.1f%% of peak)\n",
                     o.variant.c_str(), o.batch, o.heads, o.seqlen, o.head_dim, causal ? 1 : 0,
-                    tile.block_q, tile.block_k, tile.waves, max_err, median, tf,
+                    tile.block_q, tile.block_k, tile.waves, tile.schedule, max_err, median, tf,
                     100.0 * tf / kPeakTflops);
     }
     if (!ok) std::printf("FAILED: |err| above 2e-3 + 1e-2 |ref| on a sampled row\n");

@@ -8,13 +8,14 @@
 
 slot: one row of the tile table in csrc/flash_fwd.hip, named after its macro (see SLOTS):
       opt_d64[_causal]_small, opt_d128[_causal]_small, opt_d64[_causal]_tiny,
-      opt_d128[_causal]_tiny, opt_d64, opt_d64_causal,
-      opt_d128_short, opt_d128, opt_d128_causal_short, opt_d128_causal, base_d64, base_d128
+      opt_d128[_causal]_tiny, opt_d64, opt_d64_causal_short, opt_d64_causal,
+      opt_d128[_causal]_vshort, opt_d128[_causal]_short, opt_d128[_causal], base_d64, base_d128
 cand: "BC,NW,LAZY,SCHED" -- keys per tile, query waves per workgroup (BR = 32 * NW), lazy
-      rescale (true/false) and schedule (SIMPLE; KSPLIT / KSPLIT4, which run two / four waves
-      per query wave; or PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves, BC=32 at D=128,
-      BC=64 at D=64), e.g. 32,8,true,PINGPONG16. Without candidates a default list for the slot
-      is used.
+      rescale (true/false) and schedule (SIMPLE on 32x32x16 MFMAs; SIMPLE16, the same schedule
+      on 16x16x32 MFMAs; KSPLIT / KSPLIT4, which run two / four waves per query wave; or
+      PINGPONG16, the ping-pong on 16x16x32 MFMAs: 8 waves; the 16x16x32 schedules take BC=32
+      at D=128 and BC=64 at D=64), e.g. 32,8,true,PINGPONG16. Without candidates a default list
+      for the slot is used.
 
 `build` compiles csrc/flash_fwd.hip once per candidate with the slot's macro overridden, into
 dev/_tune/<slot>/<cand>.so (candidates the tile checks reject fail to compile and are reported
@@ -64,21 +65,35 @@ SLOTS = {
     "opt_d128_tiny": ("FA_OPT_D128_TINY", "opt", 128, 0, _TINY),
     "opt_d128_causal_tiny": ("FA_OPT_D128_TINY", "opt", 128, 1, _TINY),
     "opt_d64": ("FA_OPT_D64", "opt", 64, 0, _BIG),
-    "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1, _BIG),
-    "opt_d128_short": ("FA_OPT_D128_SHORT", "opt", 128, 0, [*_BIG, f"-DFA_D128_SHORT_MAX_N={_ALL}"]),
-    "opt_d128": ("FA_OPT_D128", "opt", 128, 0, [*_BIG, f"-DFA_D128_SHORT_MAX_N={_NONE}"]),
+    "opt_d64_causal_short": ("FA_OPT_D64_CAUSAL_SHORT", "opt", 64, 1,
+                             [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_ALL}"]),
+    "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1,
+                       [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_NONE}"]),
+    "opt_d128_vshort": ("FA_OPT_D128_VSHORT", "opt", 128, 0,
+                        [*_BIG, f"-DFA_D128_VSHORT_MAX_N={_ALL}"]),
+    "opt_d128_short": ("FA_OPT_D128_SHORT", "opt", 128, 0,
+                       [*_BIG, f"-DFA_D128_VSHORT_MAX_N={_NONE}",
+                        f"-DFA_D128_SHORT_MAX_N={_ALL}"]),
+    "opt_d128": ("FA_OPT_D128", "opt", 128, 0,
+                 [*_BIG, f"-DFA_D128_VSHORT_MAX_N={_NONE}", f"-DFA_D128_SHORT_MAX_N={_NONE}"]),
+    "opt_d128_causal_vshort": ("FA_OPT_D128_CAUSAL_VSHORT", "opt", 128, 1,
+                               [*_BIG, f"-DFA_D128_CAUSAL_VSHORT_MAX_N={_ALL}"]),
     "opt_d128_causal_short": ("FA_OPT_D128_CAUSAL_SHORT", "opt", 128, 1,
-                              [*_BIG, f"-DFA_D128_CAUSAL_SHORT_MAX_N={_ALL}"]),
+                              [*_BIG, f"-DFA_D128_CAUSAL_VSHORT_MAX_N={_NONE}",
+                               f"-DFA_D128_CAUSAL_SHORT_MAX_N={_ALL}"]),
     "opt_d128_causal": ("FA_OPT_D128_CAUSAL", "opt", 128, 1,
-                        [*_BIG, f"-DFA_D128_CAUSAL_SHORT_MAX_N={_NONE}"]),
+                        [*_BIG, f"-DFA_D128_CAUSAL_VSHORT_MAX_N={_NONE}",
+                         f"-DFA_D128_CAUSAL_SHORT_MAX_N={_NONE}"]),
     "base_d64": ("FA_BASE_D64", "base", 64, 0, []),
     "base_d128": ("FA_BASE_D128", "base", 128, 0, []),
 }
 DEFAULT_CANDS = {
-    64: ["64,8,true,PINGPONG16", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE",
-         "64,4,false,SIMPLE", "64,2,true,KSPLIT", "32,2,true,KSPLIT", "64,2,true,KSPLIT4"],
-    128: ["32,8,true,PINGPONG16", "32,4,true,SIMPLE", "64,4,true,SIMPLE", "64,8,true,SIMPLE",
-          "64,4,false,SIMPLE", "32,2,true,KSPLIT", "32,4,true,KSPLIT", "32,2,true,KSPLIT4"],
+    64: ["64,8,true,PINGPONG16", "64,8,true,SIMPLE16", "64,4,true,SIMPLE16", "32,4,true,SIMPLE",
+         "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "64,2,true,KSPLIT",
+         "32,2,true,KSPLIT", "64,2,true,KSPLIT4"],
+    128: ["32,8,true,PINGPONG16", "32,4,true,SIMPLE16", "32,8,true,SIMPLE16", "32,4,true,SIMPLE",
+          "64,4,true,SIMPLE", "64,8,true,SIMPLE", "64,4,false,SIMPLE", "32,2,true,KSPLIT",
+          "32,4,true,KSPLIT", "32,2,true,KSPLIT4"],
 }
 
 

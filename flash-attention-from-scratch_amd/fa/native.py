@@ -43,7 +43,12 @@ class FaTileInfo(ctypes.Structure):
         ("block_k", ctypes.c_int32),
         ("waves", ctypes.c_int32),
         ("lds_bytes", ctypes.c_int32),
+        ("schedule", ctypes.c_int32),
     ]
+
+
+# fa_schedule (include/fa_hip.h): the main-loop schedule of a tile, by name.
+SCHEDULES = {0: "simple", 3: "ksplit", 4: "pingpong16", 5: "ksplit4", 6: "simple16"}
 
 
 class FaSplitKvInfo(ctypes.Structure):
@@ -169,7 +174,7 @@ def tile_config(head_dim: int, causal: bool, variant: str | int = "opt",
     if rc != FA_OK:
         raise ValueError(so.fa_last_error().decode())
     return {"block_q": info.block_q, "block_k": info.block_k, "waves": info.waves,
-            "lds_bytes": info.lds_bytes}
+            "lds_bytes": info.lds_bytes, "schedule": SCHEDULES[info.schedule]}
 
 
 def version() -> str:

@@ -134,17 +134,31 @@ int fa_flash_fwd_splitkv(const fa_params* params, float* lse, int32_t num_splits
 int fa_flash_fwd_splitkv_static(const fa_params* params, float* lse, int32_t num_splits,
                                 void* stream);
 
+/* Main-loop schedule of a tile (fa_tile_info.schedule). */
+typedef enum fa_schedule {
+    FA_SCHED_SIMPLE = 0,     /* each wave runs S = QK^T, softmax and O += PV of a tile in turn,
+                                on 32x32x16 MFMAs                                             */
+    FA_SCHED_KSPLIT = 3,     /* small grids: two waves per 32 query rows, each on every second
+                                key tile, merged through LDS                                  */
+    FA_SCHED_PINGPONG16 = 4, /* two groups of waves alternate between an MFMA-only phase and a
+                                softmax phase, on 16x16x32 MFMAs                               */
+    FA_SCHED_KSPLIT4 = 5,    /* tiny grids: four waves per 32 query rows                       */
+    FA_SCHED_SIMPLE16 = 6    /* the simple schedule on 16x16x32 MFMAs                          */
+} fa_schedule;
+
 /* Tile geometry fa_flash_fwd launches for these parameters: query rows per workgroup, keys per
- * tile, wavefronts per workgroup and LDS bytes per workgroup. The choice depends on variant,
- * head_dim, causal, seqlen and batch * heads (small grids get smaller workgroups); the four
- * pointers are not read. Host-only, touches no device. No counterpart function in the
- * reference, whose tiles are compile-time `using` lines (csrc/kernels/flash_fwd.cu:597-612);
- * exported so that tests and the benchmark can report and check the grid the kernel runs. */
+ * tile, wavefronts per workgroup, LDS bytes per workgroup and the main-loop schedule. The
+ * choice depends on variant, head_dim, causal, seqlen and batch * heads (small grids get
+ * smaller workgroups); the four pointers are not read. Host-only, touches no device. No
+ * counterpart function in the reference, whose tiles are compile-time `using` lines
+ * (csrc/kernels/flash_fwd.cu:597-612); exported so that tests and the benchmark can report and
+ * check the grid the kernel runs. */
 typedef struct fa_tile_info {
     int32_t block_q;       /* BR: query rows per workgroup                                     */
     int32_t block_k;       /* BC: key rows per K/V tile                                        */
     int32_t waves;         /* wavefronts (64 lanes) per workgroup                              */
     int32_t lds_bytes;     /* LDS per workgroup                                                */
+    int32_t schedule;      /* an fa_schedule value                                             */
 } fa_tile_info;
 int fa_tile_config(const fa_params* params, fa_tile_info* out);
 

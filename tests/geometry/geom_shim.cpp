@@ -30,6 +30,10 @@ int geom_swizzle_chunk_m16(int row, int chunk, int d) { return g::swizzle_chunk_
 int geom_tile_offset_m16(int row, int chunk, int d) { return g::tile_offset_m16(row, chunk, d); }
 int geom_st16_key(int lane, int kb, int r) { return g::st16_key(lane, kb, r); }
 int geom_st16_query(int lane, int qb) { return g::st16_query(lane, qb); }
+int geom_st16_key_lane(int lane) { return g::st16_key_lane(lane); }
+int geom_st16_mask_limit(int n, int kt, int qw, int lane, int qb, int causal) {
+    return g::st16_mask_limit(n, kt, qw, lane, qb, causal != 0);
+}
 int geom_pv16_key(int lane, int t, int i) { return g::pv16_key(lane, t, i); }
 int geom_pv_key(int lane, int i) { return g::pv_key(lane, i); }
 int geom_num_kv_tiles(int n, int q0, int block_q, int block_k, int causal) {

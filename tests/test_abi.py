@@ -101,7 +101,7 @@ def test_null_params_and_reserved_bytes():
 
 def _tile(d, causal, var, n, b=16, h=32):
     t = native.tile_config(d, causal, var, n, b, h)
-    return t["block_q"], t["block_k"], t["waves"], t["lds_bytes"]
+    return t["block_q"], t["block_k"], t["waves"], t["lds_bytes"], t["schedule"]
 
 
 def test_tile_config_invariants():
@@ -110,48 +110,51 @@ def test_tile_config_invariants():
             for var in ("baseline", "opt", "fp16acc"):
                 for n in (1, 1000, 2048, 2049, 3072, 3073, 4096, 4097, 8192, 8193, 16384):
                     for b, h in ((1, 1), (2, 8), (16, 32)):
-                        bq, bk, waves, lds = _tile(d, causal, var, n, b, h)
+                        bq, bk, waves, lds, sched = _tile(d, causal, var, n, b, h)
                         # 32 query rows per wave, or per two or four waves (key split)
-                        assert bq in (32 * waves, 16 * waves, 8 * waves) and bk % 32 == 0
+                        split = {"ksplit": 2, "ksplit4": 4}.get(sched, 1)
+                        assert bq == 32 * waves // split and bk % 32 == 0
                         # two or three K/V tile buffers each, per key part
-                        assert lds in (4 * bk * 2 * d, 6 * bk * 2 * d, 8 * bk * 2 * d,
-                                       16 * bk * 2 * d)
+                        assert lds in (4 * bk * 2 * d * split, 6 * bk * 2 * d * split)
                         # above 64 KiB only the four-way key split (one workgroup per CU)
-                        assert lds <= 64 * 1024 or (bq == 8 * waves and lds <= 160 * 1024)
+                        assert lds <= 64 * 1024 or (sched == "ksplit4" and lds <= 160 * 1024)
+                        # the 16x16x32 layouts: 32-key tiles at d=128, 64-key tiles at d=64
+                        if sched in ("simple16", "pingpong16"):
+                            assert bk == 4096 // d
                         assert _tile(d, causal, "fp16acc", n, b, h) == _tile(d, causal, "opt", n, b, h)
 
 
 def test_tile_config_rows():
     """The opt rows by N for a large grid (16 x 32 heads), and the small-grid rows."""
-    simple64x8, simple128x4 = (256, 64, 8, 32768), (128, 32, 4, 32768)
-    pingpong64 = (256, 64, 8, 49152)                                   # three K + three V tiles
-    for n in (1, 2048, 4095):                                          # d=64, short: simple
-        assert _tile(64, False, "opt", n) == simple64x8
-    for n in (1, 2048, 4096, 8191):
+    simple64x8, simple16_64x8 = (256, 64, 8, 32768, "simple"), (256, 64, 8, 32768, "simple16")
+    simple128x4, simple16_128x4 = (128, 32, 4, 32768, "simple"), (128, 32, 4, 32768, "simple16")
+    pingpong128 = (256, 32, 8, 49152, "pingpong16")                   # three K + three V tiles
+    for n in (1, 2048, 4096, 8192, 16384):                            # d=64: simple16 ...
+        assert _tile(64, False, "opt", n) == simple16_64x8
+    for n in (1, 2048):                                               # ... causal from 2049 keys
         assert _tile(64, True, "opt", n) == simple64x8
-    # from 4096 keys (causal 8192) the ping-pong, where its rounds of one workgroup per CU are
-    # (nearly) full: 16 x 32 heads give 512 * ceil(N / 256) items, whole rounds of 256
-    for n in (4096, 4097, 8193, 16384):
-        assert _tile(64, False, "opt", n) == pingpong64
-    assert _tile(64, True, "opt", 16384) == pingpong64                  # 4096 pairs
-    assert _tile(64, False, "opt", 6144, 3, 16) == simple64x8          # 1152 items: 4.5 rounds
-    assert _tile(64, True, "opt", 12288, 1, 16) == simple64x8          # 384 pairs: 1.5 rounds
-    assert _tile(128, False, "opt", 768) == simple128x4
-    assert _tile(128, False, "opt", 769) == (256, 32, 8, 49152)        # ping-pong
-    assert _tile(128, True, "opt", 2048) == simple128x4
-    assert _tile(128, True, "opt", 2049) == (256, 32, 8, 49152)
+    for n in (2049, 4096, 16384):
+        assert _tile(64, True, "opt", n) == simple16_64x8
+    assert _tile(128, False, "opt", 256) == simple128x4
+    assert _tile(128, False, "opt", 257) == simple16_128x4
+    assert _tile(128, False, "opt", 768) == simple16_128x4
+    assert _tile(128, False, "opt", 769) == pingpong128
+    assert _tile(128, True, "opt", 512) == simple128x4
+    assert _tile(128, True, "opt", 513) == simple16_128x4
+    assert _tile(128, True, "opt", 2048) == simple16_128x4
+    assert _tile(128, True, "opt", 2049) == pingpong128
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
     # two waves on each 32 rows)
-    assert _tile(64, True, "opt", 900, 2, 8) == (64, 64, 4, 65536)
+    assert _tile(64, True, "opt", 900, 2, 8) == (64, 64, 4, 65536, "ksplit")
     # at most 256 query blocks of 64 rows and at least 16 key tiles: four waves per 32 rows
-    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 8, 131072)
-    assert _tile(128, False, "opt", 1500, 1, 2) == (64, 32, 8, 131072)
-    assert _tile(64, False, "opt", 256, 1, 4) == (64, 64, 4, 65536)
-    assert _tile(128, False, "opt", 16384, 1, 3) == (64, 32, 4, 65536)
-    assert _tile(128, True, "opt", 16384, 1, 3) == (64, 32, 4, 65536)
-    assert _tile(128, False, "opt", 16384, 1, 4) == (256, 32, 8, 49152)  # 4 * 64 = 256 WGs
+    assert _tile(64, True, "opt", 1000, 2, 8) == (64, 64, 8, 131072, "ksplit4")
+    assert _tile(128, False, "opt", 1500, 1, 2) == (64, 32, 8, 131072, "ksplit4")
+    assert _tile(64, False, "opt", 256, 1, 4) == (64, 64, 4, 65536, "ksplit")
+    assert _tile(128, False, "opt", 16384, 1, 3) == (64, 32, 4, 65536, "ksplit")
+    assert _tile(128, True, "opt", 16384, 1, 3) == (64, 32, 4, 65536, "ksplit")
+    assert _tile(128, False, "opt", 16384, 1, 4) == pingpong128        # 4 * 64 = 256 WGs
     for n in (1, 5000, 16384):
-        assert _tile(64, n > 1, "baseline", n) == (128, 64, 4, 32768)
+        assert _tile(64, n > 1, "baseline", n) == (128, 64, 4, 32768, "simple")
 
 
 def test_tile_config_errors():

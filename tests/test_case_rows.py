@@ -19,17 +19,19 @@ import test_tile_rows as rows
 
 def _tile(b, h, n, d, causal, variant="opt"):
     t = native.tile_config(d, causal, variant, n, b, h)
-    return t["block_q"], t["block_k"], t["waves"], t["lds_bytes"]
+    return t["block_q"], t["block_k"], t["waves"], t["lds_bytes"], t["schedule"]
 
 
 # Every (head_dim, causal, tile) the opt table can pick: the key split for small grids, the
-# simple tile, and the ping-pong (d=64: long sequences with full rounds).
+# simple schedule on 32x32x16 MFMAs (d=64 causal up to 2048 keys, d=128 up to 256 keys, causal
+# 512) or on 16x16x32 MFMAs, and the d=128 ping-pong.
 OPT_ROWS = {
     (64, False, rows.SMALL64), (64, True, rows.SMALL64),
-    (64, False, rows.SIMPLE64X8), (64, True, rows.SIMPLE64X8),
-    (64, False, rows.PP64), (64, True, rows.PP64),
+    (64, True, rows.SIMPLE64X8),
+    (64, False, rows.S16_64X8), (64, True, rows.S16_64X8),
     (128, False, rows.SMALL128), (128, True, rows.SMALL128),
     (128, False, rows.SIMPLE128X4), (128, True, rows.SIMPLE128X4),
+    (128, False, rows.S16_128X4), (128, True, rows.S16_128X4),
     (128, False, rows.PP128), (128, True, rows.PP128),
     (64, False, rows.TINY64), (64, True, rows.TINY64),
     (128, False, rows.TINY128), (128, True, rows.TINY128),
@@ -45,9 +47,10 @@ def test_row_cases_cover_every_opt_row():
     assert {(d, c, w) for _, _, _, d, c, w in rows.ROWS} == OPT_ROWS
 
 
-def test_pingpong_cases_select_the_pingpong():
-    for b, h, n, causal in rows.PP_SCALE_CASES:
-        assert _tile(b, h, n, 128, causal) == rows.PP128
+def test_m16_scale_cases_select_their_rows():
+    for b, h, n, d, causal, want in rows.M16_SCALE_CASES:
+        assert _tile(b, h, n, d, causal) == want
+        assert want[4] in ("pingpong16", "simple16")
 
 
 @pytest.mark.parametrize("n", [1, 17, 65, 257, 1000])

@@ -432,6 +432,57 @@ def test_score_mask_threshold_catches_a_dropped_bound(geo):
         assert found, bad.__name__
 
 
+def test_st16_key_splits_into_lane_and_accumulator_parts(geo):
+    for lane, kb, r in itertools.product(range(64), range(4), range(4)):
+        assert geo.geom_st16_key(lane, kb, r) == (geo.geom_st16_key(0, kb, r)
+                                                   + geo.geom_st16_key_lane(lane))
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_score_mask_threshold_16x16(geo, causal):
+    """The simple schedule on 16x16x32 MFMAs masks accumulator r of block (kb, qb) of `lane` iff
+    st16_key(0, kb, r) > st16_mask_limit(...): exactly "key >= n, or (causal) key right of the
+    query" for every lane, block, accumulator, tile and wave of a tile that is masked (64-key
+    tiles at d=64, 32-key tiles at d=128)."""
+    k0 = {(kb, r): geo.geom_st16_key(0, kb, r) for kb in range(4) for r in range(4)}
+    lane_key = {(lane, kb, r): geo.geom_st16_key(lane, kb, r)
+                for lane in range(64) for kb in range(4) for r in range(4)}
+    for n, bk in itertools.product([1, 17, 64, 65, 100, 200], [32, 64]):
+        for qw in range(0, n + 32, 32):
+            for kt in range(0, n + bk, bk):
+                for lane, qb in itertools.product(range(64), range(2)):
+                    query = qw + geo.geom_st16_query(lane, qb)
+                    lim = geo.geom_st16_mask_limit(n, kt, qw, lane, qb, causal)
+                    for kb, r in itertools.product(range(bk // 16), range(4)):
+                        key = kt + lane_key[(lane, kb, r)]
+                        want = key >= n or (causal and key > query)
+                        assert (k0[(kb, r)] > lim) == want, (n, bk, qw, kt, lane, qb, kb, r)
+
+
+def test_score_mask_threshold_16x16_catches_a_wrong_query(geo):
+    """Planted on the CPU: a threshold that takes the query of block 0 for block 1 (or the
+    32x32 layout's lane part) must disagree with the direct predicate somewhere."""
+    def lim_block0(n, kt, qw, lane, qb):
+        return geo.geom_st16_mask_limit(n, kt, qw, lane, 0, 1)
+
+    def lim_lane32(n, kt, qw, lane, qb):
+        return (geo.geom_st16_mask_limit(n, kt, qw, lane, qb, 1) + geo.geom_st16_key_lane(lane)
+                - geo.geom_st_key_lane(lane))
+
+    for bad in (lim_block0, lim_lane32):
+        found = False
+        for kt, lane, qb, kb, r in itertools.product([0, 32], range(64), range(2), range(4),
+                                                     range(4)):
+            n, qw = 200, 32
+            query = qw + geo.geom_st16_query(lane, qb)
+            key = kt + geo.geom_st16_key(lane, kb, r)
+            want = key >= n or key > query
+            if (geo.geom_st16_key(0, kb, r) > bad(n, kt, qw, lane, qb)) != want:
+                found = True
+                break
+        assert found, bad.__name__
+
+
 @pytest.mark.parametrize("causal", [0, 1])
 def test_work_map_is_a_bijection(geo, causal):
     for bhc, nqb in [(1, 1), (6, 9), (16, 128), (512, 16)]:

@@ -19,7 +19,7 @@ import pytest
 RES = Path(__file__).resolve().parents[1] / "flash-attention-from-scratch_amd" / "fa" / \
     "libfa_hip.resources.json"
 TILE = re.compile(r"TileILi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d)E")
-SIMPLE, KSPLIT, PINGPONG16, KSPLIT4 = 0, 3, 4, 5
+SIMPLE, KSPLIT, PINGPONG16, KSPLIT4, SIMPLE16 = 0, 3, 4, 5, 6
 
 
 def _load():
@@ -45,14 +45,14 @@ def _min_occupancy(name: str) -> int:
         return 2                      # waves w and w+4 share a SIMD
     if family == "flash_fwd_ksplit":
         return 2                      # two 4-wave workgroups (64 KiB) or one 8-wave (128 KiB)
-    assert family == "flash_fwd_kernel" and sched == SIMPLE, name
+    assert (family, sched) in (("flash_fwd_kernel", SIMPLE), ("flash_fwd_simple16", SIMPLE16)), name
     return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
 
 
 def test_every_kernel_is_recorded():
     families = {_family(k) for k in _load()}
-    assert families == {"flash_fwd_kernel", "flash_fwd_pingpong16", "flash_fwd_ksplit",
-                        "flash_fwd_combine"}, families
+    assert families == {"flash_fwd_kernel", "flash_fwd_simple16", "flash_fwd_pingpong16",
+                        "flash_fwd_ksplit", "flash_fwd_combine"}, families
 
 
 def test_no_kernel_spills_to_scratch():

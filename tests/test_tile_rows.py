@@ -29,7 +29,7 @@ def _check(b, h, n, d, causal, want, seed=11):
     from fa import native
 
     tile = native.tile_config(d, causal, "opt", n, b, h)
-    got = (tile["block_q"], tile["block_k"], tile["waves"], tile["lds_bytes"])
+    got = (tile["block_q"], tile["block_k"], tile["waves"], tile["lds_bytes"], tile["schedule"])
     print(f"case B={b} H={h} N={n} d={d} causal={causal} tile={got}", flush=True)
     assert got == want, (got, want)
     g = torch.Generator().manual_seed(seed)
@@ -41,14 +41,16 @@ def _check(b, h, n, d, causal, want, seed=11):
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
 
 
-PP128 = (256, 32, 8, 49152)      # ping-pong, d=128
-PP64 = (256, 64, 8, 49152)       # ping-pong, d=64 (long sequences, full rounds)
-SIMPLE64X8 = (256, 64, 8, 32768)
-SIMPLE128X4 = (128, 32, 4, 32768)
-SMALL64 = (64, 64, 4, 65536)     # key split: 64 rows, 2 x 2 waves, BC=64
-SMALL128 = (64, 32, 4, 65536)    # key split: 64 rows, 2 x 2 waves, BC=32
-TINY64 = (64, 64, 8, 131072)     # four-way key split: 64 rows, 4 x 2 waves, BC=64
-TINY128 = (64, 32, 8, 131072)    # four-way key split: 64 rows, 4 x 2 waves, BC=32
+# (block_q, block_k, waves, lds_bytes, schedule)
+PP128 = (256, 32, 8, 49152, "pingpong16")      # ping-pong, d=128
+SIMPLE64X8 = (256, 64, 8, 32768, "simple")     # 32x32x16 MFMAs
+S16_64X8 = (256, 64, 8, 32768, "simple16")     # the simple schedule on 16x16x32 MFMAs
+SIMPLE128X4 = (128, 32, 4, 32768, "simple")
+S16_128X4 = (128, 32, 4, 32768, "simple16")
+SMALL64 = (64, 64, 4, 65536, "ksplit")         # key split: 64 rows, 2 x 2 waves, BC=64
+SMALL128 = (64, 32, 4, 65536, "ksplit")        # key split: 64 rows, 2 x 2 waves, BC=32
+TINY64 = (64, 64, 8, 131072, "ksplit4")        # four-way key split: 64 rows, 4 x 2 waves, BC=64
+TINY128 = (64, 32, 8, 131072, "ksplit4")       # four-way key split: 64 rows, 4 x 2 waves, BC=32
 
 ROWS = [
     # (B, H, N, d, causal, expected tile)
@@ -60,16 +62,17 @@ ROWS = [
     (1, 12, 1500, 128, True, SMALL128),
     (1, 2, 1500, 128, False, TINY128),
     (1, 2, 1500, 128, True, TINY128),
-    (4, 16, 1000, 64, False, SIMPLE64X8),
-    (1, 32, 2500, 64, False, SIMPLE64X8),
+    (4, 16, 1000, 64, False, S16_64X8),
+    (1, 32, 2500, 64, False, S16_64X8),
+    (1, 8, 8000, 64, False, S16_64X8),
     (4, 16, 1000, 64, True, SIMPLE64X8),
-    (1, 8, 8500, 64, True, PP64),             # 136 pairs: one round
-    (1, 16, 12288, 64, True, SIMPLE64X8),     # 384 pairs would run 1.5 rounds
-    (1, 8, 8000, 64, False, PP64),            # 256 items: one full round
-    (3, 16, 6100, 64, False, SIMPLE64X8),     # 1152 items: 4.5 rounds
-    (8, 16, 700, 128, False, SIMPLE128X4),
+    (1, 32, 2500, 64, True, S16_64X8),
+    (1, 8, 8500, 64, True, S16_64X8),
+    (16, 16, 250, 128, False, SIMPLE128X4),
+    (8, 16, 700, 128, False, S16_128X4),
     (2, 16, 2500, 128, False, PP128),
-    (4, 16, 1000, 128, True, SIMPLE128X4),
+    (16, 16, 500, 128, True, SIMPLE128X4),
+    (4, 16, 1000, 128, True, S16_128X4),
     (1, 16, 4000, 128, True, PP128),
 ]
 
@@ -80,19 +83,19 @@ def test_row(b, h, n, d, causal, want):
 
 
 SWITCHES = [
-    (4, 32, 768, 128, False, SIMPLE128X4), (4, 32, 769, 128, False, PP128),
-    (1, 32, 2048, 128, True, SIMPLE128X4), (1, 32, 2049, 128, True, PP128),
+    (8, 32, 256, 128, False, SIMPLE128X4), (8, 32, 257, 128, False, S16_128X4),
+    (4, 32, 768, 128, False, S16_128X4), (4, 32, 769, 128, False, PP128),
+    (4, 32, 512, 128, True, SIMPLE128X4), (4, 32, 513, 128, True, S16_128X4),
+    (1, 32, 2048, 128, True, S16_128X4), (1, 32, 2049, 128, True, PP128),
+    (4, 16, 2048, 64, True, SIMPLE64X8), (4, 16, 2049, 64, True, S16_64X8),
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
-    (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, SIMPLE64X8),
+    (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, S16_64X8),
     # four-way split: at most 256 query blocks of 64 rows and at least 16 key tiles
     (1, 16, 1024, 64, False, TINY64), (1, 17, 1024, 64, False, SMALL64),
     (1, 16, 960, 64, True, SMALL64), (1, 16, 961, 64, True, TINY64),
     (1, 16, 1024, 128, True, TINY128), (1, 17, 1024, 128, True, SMALL128),
     (1, 16, 480, 128, False, SMALL128), (1, 16, 481, 128, False, TINY128),
-    # d=64 ping-pong from 4096 keys (causal 8192)
-    (1, 16, 4095, 64, False, SIMPLE64X8), (1, 16, 4096, 64, False, PP64),
-    (1, 16, 8191, 64, True, SIMPLE64X8), (1, 16, 8192, 64, True, PP64),
 ]
 
 
@@ -140,22 +143,28 @@ def test_more_heads_than_the_reference_grid_limit(d, causal):
 
 
 PP_SCALE_CASES = [(4, 16, 1100, False), (2, 16, 3100, True)]
+# (B, H, N, d, causal, tile): the rows on 16x16x32 MFMAs
+M16_SCALE_CASES = [(b, h, n, 128, c, PP128) for b, h, n, c in PP_SCALE_CASES] + [
+    (4, 16, 1100, 64, False, S16_64X8), (2, 16, 3100, 64, True, S16_64X8),
+    (8, 16, 700, 128, False, S16_128X4), (4, 16, 1500, 128, True, S16_128X4),
+]
 
 
-@pytest.mark.parametrize("b,h,n,causal", PP_SCALE_CASES)
+@pytest.mark.parametrize("b,h,n,d,causal,want", M16_SCALE_CASES)
 @pytest.mark.parametrize("scale", [0.3, -0.2, 0.0, 1.5])
-def test_pingpong16_scales_and_lse(b, h, n, causal, scale):
-    """The d=128 ping-pong row (16x16x32 MFMAs) with custom, negative (Q negated), zero and
-    large softmax scales, O and the row LSE, against the oracle."""
+def test_m16_rows_scales_and_lse(b, h, n, d, causal, want, scale):
+    """The rows on 16x16x32 MFMAs (the d=128 ping-pong, the simple schedule's SIMPLE16 rows)
+    with custom, negative (Q negated), zero and large softmax scales, O and the row LSE,
+    against the oracle."""
     import fa
     from fa import native
 
-    tile = native.tile_config(128, causal, "opt", n, b, h)
-    got = (tile["block_q"], tile["block_k"], tile["waves"], tile["lds_bytes"])
-    print(f"case B={b} H={h} N={n} causal={causal} scale={scale} tile={got}", flush=True)
-    assert got == PP128
+    tile = native.tile_config(d, causal, "opt", n, b, h)
+    got = (tile["block_q"], tile["block_k"], tile["waves"], tile["lds_bytes"], tile["schedule"])
+    print(f"case B={b} H={h} N={n} d={d} causal={causal} scale={scale} tile={got}", flush=True)
+    assert got == want
     g = torch.Generator().manual_seed(int(1000 * scale) + n)
-    q, k, v = (torch.randn(b, h, n, 128, generator=g).half() for _ in range(3))
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
     out, lse = fa.forward_lse(q.cuda(), k.cuda(), v.cuda(), causal=causal, softmax_scale=scale)
     out, lse = out.cpu(), lse.cpu()
     for bi, hi in {(0, 0), (b - 1, h - 1)}:
