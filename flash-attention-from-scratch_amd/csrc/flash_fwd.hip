@@ -2310,6 +2310,16 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
 #ifndef FA_OPT_D64
 #define FA_OPT_D64 64, 8, true, SIMPLE16
 #endif
+// Non-causal d = 64 grids of exactly one round of one workgroup per CU (B*H*ceil(N/256) = 256
+// items, which is also how the head split runs its first heads when they fill one round): the
+// simple schedule would hold one of its two workgroups per CU there, and the ping-pong, built for
+// one, is faster (1x8x8192 +9.9 %, 1x16x4096 +7.8 %, 1x4x16384 +12.9 %, 2x8x4096 +8.6 %).
+#ifndef FA_OPT_D64_ONE_ROUND
+#define FA_OPT_D64_ONE_ROUND 64, 8, true, PINGPONG16
+#endif
+#ifndef FA_D64_ONE_ROUND_MIN_N
+#define FA_D64_ONE_ROUND_MIN_N 4096
+#endif
 #ifndef FA_OPT_D64_CAUSAL_SHORT
 #define FA_OPT_D64_CAUSAL_SHORT 64, 8, true, SIMPLE
 #endif
@@ -2363,7 +2373,8 @@ enum TileId : int {
     BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
     OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
     OPT_D64_TINY, OPT_D64_C_TINY, OPT_D128_TINY, OPT_D128_C_TINY,
-    OPT_D64, OPT_D64_C_SHORT, OPT_D64_C, OPT_D128_VSHORT, OPT_D128_SHORT, OPT_D128,
+    OPT_D64, OPT_D64_ONE_ROUND, OPT_D64_C_SHORT, OPT_D64_C, OPT_D128_VSHORT, OPT_D128_SHORT,
+    OPT_D128,
     OPT_D128_C_VSHORT, OPT_D128_C_SHORT, OPT_D128_C,
 };
 template <int ID> struct Row;
@@ -2380,6 +2391,7 @@ template <> struct Row<OPT_D64_C_TINY> : Entry<Tile<64, FA_OPT_D64_TINY>, true> 
 template <> struct Row<OPT_D128_TINY> : Entry<Tile<128, FA_OPT_D128_TINY>, false> {};
 template <> struct Row<OPT_D128_C_TINY> : Entry<Tile<128, FA_OPT_D128_TINY>, true> {};
 template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
+template <> struct Row<OPT_D64_ONE_ROUND> : Entry<Tile<64, FA_OPT_D64_ONE_ROUND>, false> {};
 template <> struct Row<OPT_D64_C_SHORT> : Entry<Tile<64, FA_OPT_D64_CAUSAL_SHORT>, true> {};
 template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
 template <> struct Row<OPT_D128_VSHORT> : Entry<Tile<128, FA_OPT_D128_VSHORT>, false> {};
@@ -2407,7 +2419,10 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
         return causal ? OPT_D128_C_SMALL : OPT_D128_SMALL;
     }
     if (head_dim == 64) {
-        if (!causal) return OPT_D64;
+        if (!causal) {
+            const int64_t items = bh * ((static_cast<int64_t>(n) + 255) / 256);
+            return n >= FA_D64_ONE_ROUND_MIN_N && items <= g::kCus ? OPT_D64_ONE_ROUND : OPT_D64;
+        }
         return n <= FA_D64_CAUSAL_SHORT_MAX_N ? OPT_D64_C_SHORT : OPT_D64_C;
     }
     if (!causal) {
@@ -2435,6 +2450,7 @@ decltype(auto) with_row(TileId id, F&& f) {
         case OPT_D128_TINY: return f(Row<OPT_D128_TINY>{});
         case OPT_D128_C_TINY: return f(Row<OPT_D128_C_TINY>{});
         case OPT_D64: return f(Row<OPT_D64>{});
+        case OPT_D64_ONE_ROUND: return f(Row<OPT_D64_ONE_ROUND>{});
         case OPT_D64_C_SHORT: return f(Row<OPT_D64_C_SHORT>{});
         case OPT_D64_C: return f(Row<OPT_D64_C>{});
         case OPT_D128_VSHORT: return f(Row<OPT_D128_VSHORT>{});
@@ -2582,9 +2598,12 @@ using SplitD128C = SplitRow<Tile<128, FA_SPLIT_D128_CAUSAL>, true, FA_SPLIT_PLAN
 // Causal d = 128 on grids of fewer 256-row query blocks than CUs (the shapes fa.forward routes
 // to split-KV): the 4-wave simple tile, two or more workgroups per CU hiding each other's
 // prologue and epilogue, beats the ping-pong there (1x1x16384 +9.0 %, 1x4x8192 +11.1 %,
-// 1x2x16384 +2.1 %) and loses on larger grids (1x2x32768 -6.4 %).
+// 1x2x16384 +2.1 %) and loses on larger grids (1x2x32768 -6.4 %); on 16x16x32 MFMAs it gains
+// another 1.4-2.9 % (1x2x16384, 1x4x8192, 1x1x16384). (The other split rows keep their tiles:
+// the simple schedule on 16x16x32 MFMAs measured -4.6 to -7.4 % on the non-causal d = 64 split
+// pass, one workgroup per CU, and -7.4 to +1.7 % on the causal one.)
 #ifndef FA_SPLIT_D128_CAUSAL_SMALL
-#define FA_SPLIT_D128_CAUSAL_SMALL 32, 4, true, SIMPLE
+#define FA_SPLIT_D128_CAUSAL_SMALL 32, 4, true, SIMPLE16
 #endif
 #ifndef FA_SPLIT_PLAN_D128_CAUSAL_SMALL
 #define FA_SPLIT_PLAN_D128_CAUSAL_SMALL 1024, 512

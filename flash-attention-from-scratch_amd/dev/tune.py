@@ -64,7 +64,7 @@ SLOTS = {
     "opt_d64_causal_tiny": ("FA_OPT_D64_TINY", "opt", 64, 1, _TINY),
     "opt_d128_tiny": ("FA_OPT_D128_TINY", "opt", 128, 0, _TINY),
     "opt_d128_causal_tiny": ("FA_OPT_D128_TINY", "opt", 128, 1, _TINY),
-    "opt_d64": ("FA_OPT_D64", "opt", 64, 0, _BIG),
+    "opt_d64": ("FA_OPT_D64", "opt", 64, 0, [*_BIG, f"-DFA_D64_ONE_ROUND_MIN_N={_ALL}"]),
     "opt_d64_causal_short": ("FA_OPT_D64_CAUSAL_SHORT", "opt", 64, 1,
                              [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_ALL}"]),
     "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1,

@@ -135,6 +135,13 @@ def test_tile_config_rows():
         assert _tile(64, True, "opt", n) == simple64x8
     for n in (2049, 4096, 16384):
         assert _tile(64, True, "opt", n) == simple16_64x8
+    # one round of one workgroup per CU (256 items) from 4096 keys: the d=64 ping-pong
+    pingpong64 = (256, 64, 8, 49152, "pingpong16")
+    assert _tile(64, False, "opt", 4096, 1, 16) == pingpong64
+    assert _tile(64, False, "opt", 16384, 1, 4) == pingpong64
+    assert _tile(64, False, "opt", 4000, 1, 16) == simple16_64x8
+    assert _tile(64, False, "opt", 4096, 1, 17) == simple16_64x8
+    assert _tile(64, True, "opt", 4096, 1, 16) == simple16_64x8
     assert _tile(128, False, "opt", 256) == simple128x4
     assert _tile(128, False, "opt", 257) == simple16_128x4
     assert _tile(128, False, "opt", 768) == simple16_128x4

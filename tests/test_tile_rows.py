@@ -43,6 +43,7 @@ def _check(b, h, n, d, causal, want, seed=11):
 
 # (block_q, block_k, waves, lds_bytes, schedule)
 PP128 = (256, 32, 8, 49152, "pingpong16")      # ping-pong, d=128
+PP64 = (256, 64, 8, 49152, "pingpong16")       # ping-pong, d=64 (one round of 256 items)
 SIMPLE64X8 = (256, 64, 8, 32768, "simple")     # 32x32x16 MFMAs
 S16_64X8 = (256, 64, 8, 32768, "simple16")     # the simple schedule on 16x16x32 MFMAs
 SIMPLE128X4 = (128, 32, 4, 32768, "simple")
@@ -64,7 +65,8 @@ ROWS = [
     (1, 2, 1500, 128, True, TINY128),
     (4, 16, 1000, 64, False, S16_64X8),
     (1, 32, 2500, 64, False, S16_64X8),
-    (1, 8, 8000, 64, False, S16_64X8),
+    (1, 8, 8000, 64, False, PP64),            # 256 items: one round of one workgroup per CU
+    (1, 9, 8000, 64, False, S16_64X8),
     (4, 16, 1000, 64, True, SIMPLE64X8),
     (1, 32, 2500, 64, True, S16_64X8),
     (1, 8, 8500, 64, True, S16_64X8),
@@ -88,6 +90,9 @@ SWITCHES = [
     (4, 32, 512, 128, True, SIMPLE128X4), (4, 32, 513, 128, True, S16_128X4),
     (1, 32, 2048, 128, True, S16_128X4), (1, 32, 2049, 128, True, PP128),
     (4, 16, 2048, 64, True, SIMPLE64X8), (4, 16, 2049, 64, True, S16_64X8),
+    # d=64 ping-pong for one round of 256 items from 4096 keys
+    (1, 16, 4095, 64, False, S16_64X8), (1, 16, 4096, 64, False, PP64),
+    (1, 17, 4096, 64, False, S16_64X8), (1, 4, 16384, 64, False, PP64),
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
     (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, S16_64X8),
