@@ -6,8 +6,8 @@ Averages every counter over the attention kernel's dispatches except the first (
 checked launch, which runs on a cold cache and clock), and derives:
   * MFMA utilisation: SQ_VALU_MFMA_BUSY_CYCLES per SIMD over GRBM_GUI_ACTIVE per XCD;
   * matrix FLOPs from SQ_INSTS_MFMA (32768 FLOPs per v_mfma_f32_32x32x16_f16, 16384 per
-    v_mfma_f32_16x16x32_f16 in flash_fwd_pingpong16) against the algorithmic 4*B*H*N^2*d
-    (halved for causal): a ratio above 1 is wasted matrix work;
+    v_mfma_f32_16x16x32_f16 in flash_fwd_pingpong16 and flash_fwd_simple16) against the
+    algorithmic 4*B*H*N^2*d (halved for causal): a ratio above 1 is wasted matrix work;
   * LDS bank-conflict rate, MFMA/VALU co-execution, waits on LDS;
   * HBM bytes = FETCH_SIZE * fetch_scale + WRITE_SIZE * write_scale (KiB), against the
     algorithmic 4*B*H*N*d*2 bytes (Q, K, V read once, O written once). The scales convert the
@@ -26,8 +26,10 @@ from collections import defaultdict
 from pathlib import Path
 
 def flops_per_mfma(kernel_name: str) -> int:
-    """flash_fwd_pingpong16 issues v_mfma_f32_16x16x32_f16; the other kernels 32x32x16."""
-    return 2 * 16 * 16 * 32 if "pingpong16" in kernel_name else 2 * 32 * 32 * 16
+    """flash_fwd_pingpong16 and flash_fwd_simple16 issue v_mfma_f32_16x16x32_f16; the other
+    kernels v_mfma_f32_32x32x16_f16."""
+    m16 = "pingpong16" in kernel_name or "simple16" in kernel_name
+    return 2 * 16 * 16 * 32 if m16 else 2 * 32 * 32 * 16
 
 
 def _counters(path: Path, kernel: str) -> dict[str, float]:
