@@ -2266,11 +2266,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
 //     (4x16x4096, 2x32x8192, 1x16x16384, 1x32x16384), causal +1.6 / +6.1 / +4.0 / -0.7 %
 //     (2x16x8192, 2x32x8192, 1x32x16384, 1x16x16384). Causal at 1024 and 2048 keys it measured
 //     -1.3 to +0.8 % (and -0.8 to -2.5 % on the many-heads shape with outlier keys);
-//   * d = 128: the 16x16x32 ping-pong for long sequences; below a threshold the 4-wave simple
-//     tile, which has no pipeline prologue and epilogue per workgroup (and, when causal, fewer
-//     diagonal tiles): on 16x16x32 MFMAs above 256 keys (causal 512; +3.3 / +5.2 % at 512 /
-//     768, causal +1.0 / +2.7 / +3.8 % at 1024 / 1536 / 2048), else on 32x32x16 (-1.8 % at 256,
-//     causal -1.2 % at 512 on 16x16x32);
+//   * d = 128: the 16x16x32 ping-pong for long sequences; up to 1536 keys (causal 3072) the
+//     4-wave simple tile, which has no pipeline prologue and epilogue per workgroup (and, when
+//     causal, fewer diagonal tiles): on 16x16x32 MFMAs above 256 keys (causal 512; +3.3 / +5.2 %
+//     at 512 / 768, causal +1.0 / +2.7 / +3.8 % at 1024 / 1536 / 2048 against 32x32x16), else
+//     on 32x32x16 (-1.8 % at 256, causal -1.2 % at 512 on 16x16x32). Against the ping-pong the
+//     4-wave tile on 16x16x32 MFMAs measured +9.2 / +1.5 / -1.2 / -3.9 % at 1024 / 1536 / 2048 /
+//     4096 keys, causal +6.0 / +0.3 / -3.6 % at 3072 / 4096 / 8192;
 //   * small grids (fewer 8-wave workgroups than the 256 CUs, e.g. B*H = 16 at N = 1000): the
 //     key-split schedule with 64-row workgroups (two waves per 32 query rows, each on half the
 //     key tiles), so the same grid keeps twice the SIMDs busy.
@@ -2351,13 +2353,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
 #define FA_D128_VSHORT_MAX_N 256
 #endif
 #ifndef FA_D128_SHORT_MAX_N
-#define FA_D128_SHORT_MAX_N 768
+#define FA_D128_SHORT_MAX_N 1536
 #endif
 #ifndef FA_D128_CAUSAL_VSHORT_MAX_N
 #define FA_D128_CAUSAL_VSHORT_MAX_N 512
 #endif
 #ifndef FA_D128_CAUSAL_SHORT_MAX_N
-#define FA_D128_CAUSAL_SHORT_MAX_N 2048
+#define FA_D128_CAUSAL_SHORT_MAX_N 3072
 #endif
 #ifndef FA_SMALL_GRID_WGS
 #define FA_SMALL_GRID_WGS 256

@@ -144,12 +144,12 @@ def test_tile_config_rows():
     assert _tile(64, True, "opt", 4096, 1, 16) == simple16_64x8
     assert _tile(128, False, "opt", 256) == simple128x4
     assert _tile(128, False, "opt", 257) == simple16_128x4
-    assert _tile(128, False, "opt", 768) == simple16_128x4
-    assert _tile(128, False, "opt", 769) == pingpong128
+    assert _tile(128, False, "opt", 1536) == simple16_128x4
+    assert _tile(128, False, "opt", 1537) == pingpong128
     assert _tile(128, True, "opt", 512) == simple128x4
     assert _tile(128, True, "opt", 513) == simple16_128x4
-    assert _tile(128, True, "opt", 2048) == simple16_128x4
-    assert _tile(128, True, "opt", 2049) == pingpong128
+    assert _tile(128, True, "opt", 3072) == simple16_128x4
+    assert _tile(128, True, "opt", 3073) == pingpong128
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
     # two waves on each 32 rows)
     assert _tile(64, True, "opt", 900, 2, 8) == (64, 64, 4, 65536, "ksplit")

@@ -86,9 +86,9 @@ def test_row(b, h, n, d, causal, want):
 
 SWITCHES = [
     (8, 32, 256, 128, False, SIMPLE128X4), (8, 32, 257, 128, False, S16_128X4),
-    (4, 32, 768, 128, False, S16_128X4), (4, 32, 769, 128, False, PP128),
+    (4, 32, 1536, 128, False, S16_128X4), (4, 32, 1537, 128, False, PP128),
     (4, 32, 512, 128, True, SIMPLE128X4), (4, 32, 513, 128, True, S16_128X4),
-    (1, 32, 2048, 128, True, S16_128X4), (1, 32, 2049, 128, True, PP128),
+    (1, 32, 3072, 128, True, S16_128X4), (1, 32, 3073, 128, True, PP128),
     (4, 16, 2048, 64, True, SIMPLE64X8), (4, 16, 2049, 64, True, S16_64X8),
     # d=64 ping-pong for one round of 256 items from 4096 keys
     (1, 16, 4095, 64, False, S16_64X8), (1, 16, 4096, 64, False, PP64),
@@ -147,7 +147,7 @@ def test_more_heads_than_the_reference_grid_limit(d, causal):
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
 
 
-PP_SCALE_CASES = [(4, 16, 1100, False), (2, 16, 3100, True)]
+PP_SCALE_CASES = [(4, 16, 1700, False), (2, 16, 3300, True)]
 # (B, H, N, d, causal, tile): the rows on 16x16x32 MFMAs
 M16_SCALE_CASES = [(b, h, n, 128, c, PP128) for b, h, n, c in PP_SCALE_CASES] + [
     (4, 16, 1100, 64, False, S16_64X8), (2, 16, 3100, 64, True, S16_64X8),
