@@ -48,6 +48,11 @@ def test_row_cases_cover_every_opt_row():
     assert {(d, c, w) for _, _, _, d, c, w in rows.ROWS} == OPT_ROWS
 
 
+def test_simple16_cases_select_simple16():
+    for b, h, n, d, causal in rows.S16_CASES:
+        assert _tile(b, h, n, d, causal)[4] == "simple16"
+
+
 def test_m16_scale_cases_select_their_rows():
     for b, h, n, d, causal, want in rows.M16_SCALE_CASES:
         assert _tile(b, h, n, d, causal) == want

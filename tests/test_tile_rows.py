@@ -178,3 +178,43 @@ def test_m16_rows_scales_and_lse(b, h, n, d, causal, want, scale):
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
         ref_lse = orc.lse_fp32(q[sl], k[sl], causal=causal, scale=scale)
         torch.testing.assert_close(lse[sl], ref_lse, atol=2e-3, rtol=0)
+
+
+# (B, H, N, d, causal): the simple schedule on 16x16x32 MFMAs, one shape per kind of its rows
+S16_CASES = [(4, 16, 1100, 64, False), (4, 16, 2600, 64, True), (8, 16, 700, 128, False),
+             (4, 16, 1500, 128, True)]
+
+
+@pytest.mark.parametrize("b,h,n,d,causal", S16_CASES)
+@pytest.mark.parametrize("kind", ["jump", "spread", "sink"])
+def test_simple16_rescale_paths(b, h, n, d, causal, kind):
+    """Inputs that take the 16x16x32 simple tile off its optimistic softmax: scores that jump by
+    far more than 2^16 after 512 keys (the optimistic pass overflows, the tile is redone exactly
+    and O rescaled), q, k ~ N(0, 1.9^2) (row maxima that keep rising, in every other head), and
+    a key 0 about 13 nats above the rest (an attention sink: the first tile's max is the row's,
+    and the rest of the row lies 17-20 exp2 units below it). Three (b, h) slices against the
+    fp32 oracle."""
+    import fa
+    from fa import native
+
+    tile = native.tile_config(d, causal, "opt", n, b, h)
+    print(f"case s16 {kind} B={b} H={h} N={n} d={d} causal={causal} tile={tile}", flush=True)
+    assert tile["schedule"] == "simple16"
+    g = torch.Generator().manual_seed(n + d + len(kind))
+    q, k, v = (torch.randn(b, h, n, d, generator=g) for _ in range(3))
+    if kind == "jump":
+        k[:, :, :512] *= 0.05
+        k[:, :, 512:] *= 3.0
+    elif kind == "spread":
+        q[:, 0::2] *= 1.9
+        k[:, 0::2] *= 1.9
+    else:
+        q[..., 0] = 4.0
+        k[:, :, 0, 0] = 13.0 * d ** 0.5 / 4.0
+    q, k, v = q.half(), k.half(), v.half()
+    out = fa.forward(q.cuda(), k.cuda(), v.cuda(), causal=causal).cpu()
+    assert torch.isfinite(out).all()
+    for bi, hi in {(0, 0), (b // 2, h // 2), (b - 1, h - 1)}:
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
