@@ -156,4 +156,15 @@ __device__ __forceinline__ bool wave_any(bool pred) {
 
 __device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// x with the sign bits of its eight halves XORed with `sign` (0x80008000 negates every half,
+// exactly; 0 leaves x as it is): one v_xor per register, without a branch.
+__device__ __forceinline__ f16x8 xor_sign8(f16x8 x, unsigned sign) {
+    uint4 u = __builtin_bit_cast(uint4, x);
+    u.x ^= sign;
+    u.y ^= sign;
+    u.z ^= sign;
+    u.w ^= sign;
+    return __builtin_bit_cast(f16x8, u);
+}
+
 }  // namespace fa::dev

@@ -2181,7 +2181,14 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
         }
     }
     f16x8 qf[G::QB][G::DC];
-    load_q16<T>(q + head, qw, n, lane, negate_q, qf);
+    // (a negative scale negates Q by one sign XOR per register: load_q16's conditional negation
+    // is turned into selects here, with a wait for the Q loads early in the prologue)
+    load_q16<T>(q + head, qw, n, lane, 0, qf);
+    const unsigned qsign = negate_q != 0 ? 0x80008000U : 0U;
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb)
+#pragma unroll
+        for (int dc = 0; dc < G::DC; ++dc) qf[qb][dc] = xor_sign8(qf[qb][dc], qsign);
     const Frag16<T> fr(lane);
 
     f32x4 oacc[G::DB][G::QB];
