@@ -44,7 +44,7 @@ LSE_CASES = [
     (16, 16, 250, 128, False),                            # (on 32x32x16 and 16x16x32 MFMAs)
     (1, 16, 5000, 64, True), (2, 16, 2500, 128, False),   # simple d=64 long / ping-pong d=128
     (1, 16, 4000, 128, True),                             # ping-pong causal
-    (1, 8, 8000, 64, False),                              # simple d=64, one round
+    (1, 8, 8000, 64, False),                              # ping-pong d=64, one round
 ]
 
 
