@@ -10,7 +10,8 @@ Targets (outputs are git-ignored; they travel to the GPU box with the source tre
   oracle  oracle/liboracle_fp64.so       the C fp64 oracle (gcc), test infrastructure only
   geom    tests/geometry/libfa_geom.so   host build of the tile geometry, for the CPU tests
   dev     dev/fa_dev             standalone C++ driver (no Python) over the C ABI, for
-          rocprofv3 counter runs and tile tuning (dev/counters.sh, dev/tune.py)
+          rocprofv3 counter runs and tile tuning (dev/counters.sh, dev/tune.py); and
+          dev/tile_ceiling, the synthetic ceiling of the d=64 simple tile
 
 Counterpart of the reference's setup.py / CMakeLists.txt / Makefile build targets
 (setup.py:12-33, CMakeLists.txt:56-87, Makefile:21-32): the kernel library is compiled by
@@ -168,6 +169,8 @@ def build_dev() -> Path:
     src = PKG / "dev" / "fa_dev.cpp"
     out = src.parent / "fa_dev"
     _run([_hipcc(), *HIP_FLAGS, "-Wextra", f"-I{INCLUDE}", str(src), "-o", str(out), "-ldl"])
+    probe = PKG / "dev" / "tile_ceiling.hip"
+    _run([_hipcc(), *HIP_FLAGS, "-Wextra", str(probe), "-o", str(probe.with_suffix(""))])
     return out
 
 

@@ -1,4 +1,5 @@
-"""The standalone driver (dev/fa_dev), the counter summariser and the tuning sweep.
+"""The standalone driver (dev/fa_dev), the counter summariser, the tuning sweep and the tile
+ceiling probe (dev/tile_ceiling).
 
 CPU: argument handling of fa_dev before any device call, the summariser on a synthetic
 rocprofv3 output, and that every tuning slot names a macro of the tile table.
@@ -38,6 +39,16 @@ def test_fa_dev_rejects_bad_arguments(args, msg):
     res = subprocess.run([str(FA_DEV), *args], capture_output=True, text=True, timeout=60)
     assert res.returncode == 2
     assert msg in res.stderr
+
+
+@pytest.mark.parametrize("iters", ["0", "-3", "2000000"])
+def test_tile_ceiling_rejects_bad_iteration_counts(iters):
+    """dev/tile_ceiling checks its argument before any HIP call."""
+    probe = DEV / "tile_ceiling"
+    if not probe.exists():
+        pytest.skip("dev/tile_ceiling not built (fa_build.py --only dev)")
+    res = subprocess.run([str(probe), iters], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 1 and "usage" in res.stderr
 
 
 def _write_csv(path: Path, header: list[str], rows: list[list]):
