@@ -18,6 +18,10 @@ peak of MI355X (2516.6 TFLOPS = 256 CU x 2.4 GHz x 4096 FLOP/clk); the causal ke
 reported beside it. cpu_baseline: the fp32 oracle (oracle/attention.py, a restatement of the
 reference's fa/reference.py) timed on this host's cores on whole (b, h) slices of the same
 inputs, for a bounded time; it performs the full N^2 work even when causal.
+other_configs: after the headline measurement (outside its timed region, not part of value),
+the other compute-bound configurations (cfg2 in both modes, cfg5 with its boosted keys) timed
+the same way, 30 launches per mode after --ramp-ms of untimed ones, with the tile each one
+runs; skip with --no-others.
 """
 
 from __future__ import annotations
@@ -114,6 +118,51 @@ def traffic_from_profiles(cfg_name: str, causal: bool):
         return None
 
 
+def other_configs(headline: str, variant: str, ramp_ms: float, launches: int = 30) -> dict:
+    """cfg2 and cfg5 (the other compute-bound configurations; cfg1 and cfg3 are launch-latency
+    bound, and their Python dispatch would be timed with them): per mode, the mean launch time of
+    `launches` back-to-back calls, from HIP events on the current stream, and the tile the
+    launcher picks. Before each mode, untimed calls for at least `ramp_ms`: the GPU idles while
+    the host draws a configuration's inputs, and its clock takes a few hundred milliseconds to
+    settle again."""
+    import torch
+
+    import fa
+    from fa import native
+    from fa.configs import CONFIGS, make_inputs
+
+    out = {}
+    for name in ("cfg2", "cfg5"):
+        if name == headline:
+            continue
+        c = CONFIGS[name]
+        q, k, v = make_inputs(c)
+        for causal in c.causal:
+            ramp0 = time.perf_counter()
+            while (time.perf_counter() - ramp0) * 1e3 < ramp_ms:
+                for _ in range(4):
+                    fa.forward_variant(q, k, v, causal=causal, variant=variant)
+                torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(launches):
+                o = fa.forward_variant(q, k, v, causal=causal, variant=variant)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / launches
+            tf = c.flops(causal) / (ms * 1e-3) / 1e12
+            t = native.tile_config(c.head_dim, causal, variant, c.seqlen, c.batch, c.heads)
+            out[f"{name}_{'causal' if causal else 'non_causal'}"] = {
+                "shape": f"B={c.batch} H={c.heads} N={c.seqlen} d={c.head_dim}",
+                "launch_ms": round(ms, 4), "tflops": round(tf, 2),
+                "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
+                "finite": bool(torch.isfinite(o).all()), "schedule": t["schedule"],
+            }
+        del q, k, v
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +175,8 @@ def main() -> int:
     ap.add_argument("--config", default="cfg4")
     ap.add_argument("--variant", default="opt", choices=["baseline", "opt", "fp16acc"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the timing of the other compute-bound configurations")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="calibration only: time a plain device copy of this many bytes (the "
@@ -256,6 +307,8 @@ def main() -> int:
         "untimed_ramp": {"ms": round(args.ramp_ms, 1), "steps": ramp_steps},
         "device": torch.cuda.get_device_name(0),
     }
+    if not args.no_others:
+        result["other_configs"] = other_configs(args.config, args.variant, args.ramp_ms)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, q, k, v, args.cpu_budget)
     else:
