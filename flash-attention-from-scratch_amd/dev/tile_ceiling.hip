@@ -8,7 +8,9 @@
 // optimistic softmax (p = exp2(s * c - m), packed to fp16, row sums by v_dot2); O += V^T P^T.
 // Variants add the transposed V fragment reads from LDS (+V) and the overflow vote with its
 // exact branch (+check, never taken here), and take away the softmax (MFMA only: p = fp16(s)) or
-// the MFMAs (VALU only: s from the K fragments). The grid is 512 workgroups of 8 waves, two per
+// the MFMAs (VALU only: s from the K fragments). Two more rows start the QK^T MFMAs from a block
+// of -m (their C operand) so that the exponential needs no FMA in front of it (FULL_CMAX), with
+// and without the V reads and the vote. The grid is 512 workgroups of 8 waves, two per
 // CU and four waves per SIMD, as the d = 64 simple tile runs. Operands are pseudo-random fp16
 // values in [-2, 2]: the chip runs at its power limit and the clock depends on the switching
 // activity of the data (structured small values run faster). Not included: the K/V DMA refills,
@@ -31,7 +33,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 #define TC_LDS __attribute__((address_space(3)))
 
-enum Mode { FULL = 0, MFMA_ONLY = 1, VALU_ONLY = 2 };
+// FULL_CMAX: as FULL, but the QK^T MFMAs start from a register block that holds -m in every
+// element (C operand) instead of zero, so that they return s * c - m directly (Q taken as already
+// scaled by c) and the exponential needs no FMA in front of it.
+enum Mode { FULL = 0, MFMA_ONLY = 1, VALU_ONLY = 2, FULL_CMAX = 3 };
 
 __device__ __forceinline__ f16x8 pack8(const float* e) {
     f16x8 r;
@@ -77,7 +82,9 @@ __device__ __forceinline__ f32x4 m16(f16x8 a, f16x8 b, f32x4 c, int mode) {
     return mode == VALU_ONLY ? c : __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ float expo(float s, float c, float m, int mode) {
-    return mode == MFMA_ONLY ? s : __builtin_amdgcn_exp2f(__builtin_fmaf(s, c, -m));
+    return mode == MFMA_ONLY   ? s
+           : mode == FULL_CMAX ? __builtin_amdgcn_exp2f(s)
+                               : __builtin_amdgcn_exp2f(__builtin_fmaf(s, c, -m));
 }
 
 template <int SHAPE, bool V, bool CHK, int MODE>
@@ -105,13 +112,16 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
     float t = 0.0F;
     if constexpr (SHAPE == 32) {
         f32x16 o[2] = {};
+        f32x16 mblk;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mblk[r] = -m;
         for (int it = 0; it < iters; ++it) {
             __syncthreads();
             const _Float16* kb0 = kl + (it & 1) * 4096 + lane * 8;
             f32x16 s[2];
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-                s[nb] = f32x16{};
+                s[nb] = MODE == FULL_CMAX ? mblk : f32x16{};
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk) {
                     const f16x8 kf = *reinterpret_cast<const f16x8*>(kb0 + (nb * 4 + kk) * 512);
@@ -143,6 +153,8 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
                         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[nb][r]);
                     m = mx * c;
 #pragma unroll
+                    for (int r = 0; r < 16; ++r) mblk[r] = -m;
+#pragma unroll
                     for (int db = 0; db < 2; ++db) o[db] *= 0.5F;
                 }
             }
@@ -159,7 +171,7 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
                         o[db] = m32(vf, p[nb][h], o[db], MODE);
                         if (MODE == VALU_ONLY) o[db][h] += static_cast<float>(p[nb][h][db]);
                     }
-            m = m + 1e-7F;
+            if (MODE != FULL_CMAX) m = m + 1e-7F;
         }
 #pragma unroll
         for (int db = 0; db < 2; ++db)
@@ -167,6 +179,7 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
             for (int r = 0; r < 16; ++r) t += o[db][r];
     } else {
         f32x4 o[4][2] = {};
+        f32x4 mblk = {-m, -m, -m, -m};
         for (int it = 0; it < iters; ++it) {
             __syncthreads();
             const _Float16* kb0 = kl + (it & 1) * 4096 + lane * 8;
@@ -179,7 +192,7 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
                     kf[dc] = *reinterpret_cast<const f16x8*>(kb0 + (kb * 2 + dc) * 512);
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb) {
-                    s[kb][qb] = f32x4{};
+                    s[kb][qb] = MODE == FULL_CMAX ? mblk : f32x4{};
 #pragma unroll
                     for (int dc = 0; dc < 2; ++dc) {
                         s[kb][qb] = m16(kf[dc], b[(qb * 2 + dc) & 3], s[kb][qb], MODE);
@@ -210,6 +223,7 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
 #pragma unroll
                             for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][qb][r]);
                     m = mx * c;
+                    mblk = f32x4{-m, -m, -m, -m};
 #pragma unroll
                     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(512) void tile_loop(float* out, int iters, float c)
                         if (MODE == VALU_ONLY) o[db][qb][tt] += static_cast<float>(p[qb][tt][db]);
                     }
             }
-            m = m + 1e-7F;
+            if (MODE != FULL_CMAX) m = m + 1e-7F;
         }
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -300,6 +314,10 @@ int main(int argc, char** argv) {
         time_ms<16, false, true, FULL>(out, iters));
     row("+ V^T reads + vote", time_ms<32, true, true, FULL>(out, iters),
         time_ms<16, true, true, FULL>(out, iters));
+    row("  same, -m in the C operand", time_ms<32, true, true, FULL_CMAX>(out, iters),
+        time_ms<16, true, true, FULL_CMAX>(out, iters));
+    row("MFMA + softmax, -m in C", time_ms<32, false, false, FULL_CMAX>(out, iters),
+        time_ms<16, false, false, FULL_CMAX>(out, iters));
     check(hipFree(out), "hipFree");
     return 0;
 }
