@@ -1071,6 +1071,18 @@ __device__ __forceinline__ void note_overflow(unsigned id) {
 #endif
 static_assert(FA_PP16_UNCHECKED_MARGIN >= 0 && FA_PP16_UNCHECKED_MARGIN <= 8,
               "the lazy rescale (threshold 8) assumes the reference max is at most 8 above a key");
+// Wide-spread items run checked from the start (exp2 units; 0 = never). The unchecked tiles
+// overflow fp16 when a later key's score exceeds the first tile's row max by 16; scores whose
+// spread is wide (q, k ~ N(0, 1.6^2): a standard deviation near 3.7) reach that late in a few
+// rows, and such an item then redoes most of its work. The item's first tile votes: a row is
+// wide if each of the four lanes holding its first 32 keys sees a score range above
+// FA_PP16_SPREAD (the smallest of the four, so that one dominant key -- an attention sink, an
+// outlier -- does not count: the reference max then sits at that key and later keys rarely
+// pass it). On q, k ~ N(0, 1) no row of 2^18 reached 7.1; on N(0, 1.6^2) a fifth of the rows
+// exceed 9, so every 256-row item is flagged (tests/test_softmax_model.py).
+#ifndef FA_PP16_SPREAD
+#define FA_PP16_SPREAD 9
+#endif
 // Per-tile geometry of the 16x16x32 path: D = 128 with 32-key tiles or D = 64 with 64-key
 // tiles; either way 32 MFMAs of each kind per wave and tile and 24 fragment reads.
 template <class T>
@@ -1270,6 +1282,33 @@ __device__ __forceinline__ void softmax16_optimistic(const f32x4 (&s)[M16<T>::KB
     overflow = wave_any(!(sum[0] < INFINITY && sum[1] < INFINITY));
 #pragma unroll
     for (int qb = 0; qb < G::QB; ++qb) l_run[qb] = overflow ? l_run[qb] : l_run[qb] + sum[qb];
+}
+
+// The wide-spread vote of an item's first tile (FA_PP16_SPREAD): true, for the whole wave, if
+// for some query the smallest of the four lanes' score ranges over the tile's first 32 keys
+// (key blocks 0 and 1: lane % 16 + 16 g holds keys m16_key(kb, 4g + 0..3)) exceeds
+// FA_PP16_SPREAD exp2 units; 32 keys at either head dim, so one threshold serves both. NaN
+// scores are skipped by v_max / v_min.
+template <class T>
+__device__ __forceinline__ bool softmax16_wide(const f32x4 (&s)[M16<T>::KB][M16<T>::QB],
+                                               float scale_log2) {
+    using G = M16<T>;
+    bool wide = false;
+#pragma unroll
+    for (int qb = 0; qb < G::QB; ++qb) {
+        float hi = s[0][qb][0];
+        float lo = hi;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                hi = fmaxf(hi, s[kb][qb][r]);
+                lo = fminf(lo, s[kb][qb][r]);
+            }
+        const float range = -max_xor32(max_xor16(-(hi - lo) * scale_log2));  // min over lanes
+        wide = wide | (range > static_cast<float>(FA_PP16_SPREAD));
+    }
+    return wave_any(wide);
 }
 
 // Exact online softmax of one tile (as softmax_tile): the tile max of a query spans the four
@@ -1533,11 +1572,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     // checked pass per item, not two passes.
     constexpr bool UNCHECKED = FA_PP16_UNCHECKED;
     // Overflow flags of the unchecked run (0-1, one per chunk mod 2) and of the item's final
-    // test (2). Cleared at the start of an item's first pass; read with the lane and wave
+    // test (2), and the first tile's wide-spread vote (3, FA_PP16_SPREAD). Cleared at the start
+    // of an item's first pass; read with the lane and wave
     // registers rather than threadIdx or __syncthreads_or, which would keep the work-item ids
     // live across the item loop (past 256 VGPRs, into scratch). Accessed with flag_get and
     // flag_set (LDS instructions).
-    __shared__ int pp_flags[3];
+    __shared__ int pp_flags[4];
     // An item's first pass runs checked from the start (1) after enough overflows in this
     // launch: wave 0 reads pp_overflow_record with the item's prologue loads and writes the
     // decision here before the prologue's barrier, so that every wave takes the same one.
@@ -1618,7 +1658,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     if constexpr (FAST) {
         // cleared before the prologue's barrier; the previous pass or item read them before
         // its own final barrier
-        if (!checked_pass && wave == 0 && lane < 3) flag_set(pp_flags[lane], 0);
+        if (!checked_pass && wave == 0 && lane < 4) flag_set(pp_flags[lane], 0);
     }
     load_tile<T>(kh, 0, nk_load, kbuf(I0{}), dma_k);
     load_tile<T>(vh, 0, nk_load, vbuf(I0{}), dma);
@@ -1716,6 +1756,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
                 softmax16_tile<T, false, FA_PP16_UNCHECKED_MARGIN>(s, scale_log2, m_run, l_run,
                                                                    alpha, rescale, p);
                 if (rescale) rescale16<T>(oacc, alpha);
+                if constexpr (FA_PP16_SPREAD > 0) {
+                    // (first pass only; a causal wave votes if all its rows see the whole tile)
+                    if (!checked_pass && !start_checked && (!CAUSAL || qk >= T::BC - 1) &&
+                        softmax16_wide<T>(s, scale_log2) && lane == 0) {
+                        flag_set(pp_flags[3], 1);
+                    }
+                }
                 if constexpr (CAUSAL && SPLIT) {
                     // a split range can start right of some rows' queries: such a row sees no
                     // key in the range, and 0 keeps its later p at exp2(-inf) = 0 (and its
@@ -1795,8 +1842,12 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             // from the steps of three; causal, from the first tile that some row of the workgroup
             // must mask (keys 0..q0 are visible to every row), i.e. the diagonal band. The
             // second pass runs every steady tile checked.
+            // A wide-spread vote of the first tile (written in its softmax phase, read here after
+            // the barrier that ends both groups' first softmax phases) also runs the item checked.
+            const bool wide = FA_PP16_SPREAD > 0 && jj == 1 && !checked_pass && !start_checked &&
+                              __builtin_amdgcn_readfirstlane(flag_get(pp_flags[3])) != 0;
             const int n_free =
-                (checked_pass || start_checked)
+                (checked_pass || start_checked || wide)
                     ? 0
                     : (CAUSAL ? min(n_busy, max(0, min(q0 - key0 + 1, nk)) / T::BC) : n_busy);
             int slot = 0;
@@ -2816,7 +2867,7 @@ const char* fa_last_error(void) { return fa::g_last_error.c_str(); }
 // the ping-pong arithmetic) can read how this library was compiled.
 const char* fa_version(void) {
     return "fa_hip 0.2.0 gfx950 pp16_unchecked=" FA_STR(FA_PP16_UNCHECKED) " pp16_margin=" FA_STR(
-        FA_PP16_UNCHECKED_MARGIN);
+        FA_PP16_UNCHECKED_MARGIN) " pp16_spread=" FA_STR(FA_PP16_SPREAD);
 }
 
 int fa_tile_config(const fa_params* params, fa_tile_info* out) {

@@ -16,6 +16,9 @@ through, so that a CPU test can ask what that arithmetic loses on a given input:
 * the row sum l is the sum of the fp16 p; an infinite l sends the row to the second pass, in
   which every steady tile is checked (the kernel may also leave the first pass early; that
   changes only its cost);
+* an item whose first tile votes "wide" (`wide_rows`: some row's four lanes all see a score
+  range above FA_PP16_SPREAD) runs every steady tile checked from the start
+  (`checked_from_start`), as the second pass does;
 * O = sum p v (fp16 p times fp16 v, accumulated in fp64 here) / l, rounded to fp16.
 
 Rounding: fp16 conversion is numpy's round-to-nearest-even with subnormals, as the kernel's
@@ -33,6 +36,26 @@ BR = 256  # query rows per ping-pong workgroup (8 waves of 32)
 
 def _f16(x: np.ndarray) -> np.ndarray:
     return np.asarray(x, np.float32).astype(np.float16).astype(np.float64)
+
+
+def m16_key(kb: int, i: int) -> int:
+    """Tile row of M index i of score block kb on the 16x16x32 path (fa::geom::m16_key,
+    csrc/fa_geometry.h): two 16-key blocks per 32 keys, interleaved by 8 rows."""
+    return 32 * (kb // 2) + 8 * (kb % 2) + (i % 8) + 16 * ((i // 8) % 2)
+
+
+def wide_rows(s_first: np.ndarray, spread: float) -> np.ndarray:
+    """The first tile's wide-spread vote of flash_fwd_pingpong16 (softmax16_wide), per row.
+
+    s_first: [rows, >= 32] scores of the item's first key tile, times scale*log2(e). Lane group
+    g (lanes 16 g .. 16 g + 15) holds keys m16_key(kb, 4 g + r), r = 0..3, of score block kb (the
+    MFMA's C layout: row 4 (lane / 16) + r); the vote looks at blocks 0 and 1, the tile's first
+    32 keys, and a row is wide if each group's range (max - min) exceeds `spread`."""
+    s_first = np.asarray(s_first, np.float32)
+    groups = [s_first[:, [m16_key(kb, 4 * g + r) for kb in (0, 1) for r in range(4)]]
+              for g in range(4)]
+    ranges = np.stack([x.max(axis=1) - x.min(axis=1) for x in groups], axis=1)
+    return ranges.min(axis=1) > spread
 
 
 def _tile_classes(n: int, r: int, bc: int, causal: bool, second_pass: bool) -> list[str]:
@@ -64,12 +87,13 @@ def _tile_classes(n: int, r: int, bc: int, causal: bool, second_pass: bool) -> l
 
 
 def pp16_row(s: np.ndarray, v: np.ndarray, r: int, n: int, *, causal: bool, margin: float,
-             bc: int = 32) -> tuple[np.ndarray, dict]:
+             bc: int = 32, checked_from_start: bool = False) -> tuple[np.ndarray, dict]:
     """Output row r (fp16 values as float64, [d]) of the ping-pong arithmetic.
 
     s: row r's scores times scale*log2(e) over all n keys (float32; the model masks keys > r
-    when causal); v: [n, d] values (fp16 values). Returns (o, info) with info["l"] the row sum
-    in units of the final reference max, info["m"] that max, info["second_pass"]."""
+    when causal); v: [n, d] values (fp16 values); checked_from_start: the item's first tile voted
+    wide (`wide_rows` over its rows). Returns (o, info) with info["l"] the row sum in units of
+    the final reference max, info["m"] that max, info["second_pass"]."""
     s = np.asarray(s, np.float32).copy()
     if causal:
         s[r + 1:] = -np.inf
@@ -114,7 +138,7 @@ def pp16_row(s: np.ndarray, v: np.ndarray, r: int, n: int, *, causal: bool, marg
                 o += p @ v64[sl]
         return o, l, m
 
-    o, l, m = run(-np.inf, False)
+    o, l, m = run(-np.inf, checked_from_start)
     second = not np.isfinite(l)
     if second:
         o, l, m = run(-np.inf, True)

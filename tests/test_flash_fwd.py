@@ -177,9 +177,9 @@ def test_overflow_at_many_points(n, causal):
 @pytest.mark.parametrize("causal", [False, True])
 def test_wide_score_spread(causal):
     """q, k ~ N(0, 1.9^2): scores of standard deviation about 5 in exp2 units, whose row maxima
-    rise far above the first key tile's. The ping-pong kernels' unchecked tiles then run
-    against the first tile's max, many p overflow fp16 and many items take the second pass:
-    fp64 rows at the north-star tolerance."""
+    rise far above the first key tile's. Unchecked tiles against the first tile's max would
+    overflow fp16 late in many items; the first tile's wide-spread vote (FA_PP16_SPREAD) runs
+    these items checked from the start instead: fp64 rows at the north-star tolerance."""
     b, h, n, d = 4, 16, 4096, 128
     print(f"case spread B={b} H={h} N={n} causal={causal}", flush=True)
     q, k, v = _qkv(b, h, n, d, seed=14)
@@ -193,22 +193,25 @@ def test_wide_score_spread(causal):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_overflows_switch_later_workgroups_to_checked(causal):
-    """Inputs on which most ping-pong items overflow fp16 against their first tile's max (q, k ~
-    N(0, 1.9^2)) on a grid of several rounds (4x16x4096 d=128: 1024 workgroups, or 512 causal
-    pairs, on 256 CUs): once a few workgroups of a launch have redone an item, the ones that
-    start later run their items checked from the start (pp_overflow_record, keyed by the
-    launch). Every slice against the fp32 oracle, for two launches in a row, then a launch on
-    N(0, 1) inputs of the same shape, which must not inherit the switch's state (a new launch
-    id) and is checked the same way."""
+    """Inputs on which most ping-pong items overflow fp16 against their first tile's max without
+    a wide first tile (q, k, v ~ N(0, 1) with 1 % of the key rows x8: the first tile's vote
+    ignores one or two outliers, and a later outlier overflows) on a grid of several rounds
+    (4x16x4096 d=128: 1024 workgroups, or 512 causal pairs, on 256 CUs): once a few workgroups
+    of a launch have redone an item, the ones that start later run their items checked from the
+    start (pp_overflow_record, keyed by the launch). Every slice against the fp32 oracle, for
+    two launches in a row, then a launch on N(0, 1) inputs of the same shape, which must not
+    inherit the switch's state (a new launch id) and is checked the same way."""
     b, h, n, d = 4, 16, 4096, 128
     q, k, v = _qkv(b, h, n, d, seed=15)
-    q, k = q * 1.9, k * 1.9
+    g = torch.Generator().manual_seed(151)
+    boost = (torch.rand(b, h, n, 1, generator=g) < 0.01).half().cuda() * 7.0 + 1.0
+    k = k * boost
     ref = orc.attention_fp32(q.cpu(), k.cpu(), v.cpu(), causal=causal)
     for rep in range(2):
-        print(f"case spread switch B={b} H={h} N={n} causal={causal} launch {rep}", flush=True)
+        print(f"case outlier switch B={b} H={h} N={n} causal={causal} launch {rep}", flush=True)
         _close(_fa().forward(q, k, v, causal=causal), ref)
     q2, k2, v2 = _qkv(b, h, n, d, seed=16)
-    print(f"case plain after spread B={b} H={h} N={n} causal={causal}", flush=True)
+    print(f"case plain after outliers B={b} H={h} N={n} causal={causal}", flush=True)
     _close(_fa().forward(q2, k2, v2, causal=causal),
            orc.attention_fp32(q2.cpu(), k2.cpu(), v2.cpu(), causal=causal))
 

@@ -348,6 +348,24 @@ def test_m16_score_blocks_cover_the_tile_once(geo, d):
         assert geo.geom_st16_key(lane, kb, r) == geo.geom_m16_key(kb, geo.geom_mfma16_c_row(lane, r))
 
 
+def test_spread_vote_model_uses_the_kernels_lane_groups(geo):
+    """The CPU model of the ping-pong's first-tile vote (tests/pp16_softmax_model.py) groups a
+    row's first 32 keys as the kernel's lanes hold them: lanes 16 g .. 16 g + 15 hold keys
+    st16_key(lane, kb, r) of blocks kb = 0, 1 (the same for all 16 lanes of a group), and the
+    four groups split the 32 keys."""
+    from pp16_softmax_model import m16_key
+
+    for kb, i in itertools.product(range(4), range(16)):
+        assert m16_key(kb, i) == geo.geom_m16_key(kb, i)
+    groups = []
+    for g in range(4):
+        keys = {geo.geom_st16_key(16 * g + x, kb, r) for x in range(16) for kb in (0, 1)
+                for r in range(4)}
+        assert keys == {m16_key(kb, 4 * g + r) for kb in (0, 1) for r in range(4)}, g
+        groups.append(keys)
+    assert sorted(k for grp in groups for k in grp) == list(range(32))
+
+
 def test_mfma_c_layouts_cover_each_cell_once(geo):
     cells = {(geo.geom_mfma32_c_row(l, r), geo.geom_mfma32_c_col(l))
              for l in range(64) for r in range(16)}

@@ -22,7 +22,7 @@ import torch
 
 from conftest import ATOL, RTOL
 from oracle import attention as orc
-from pp16_softmax_model import pp16_row
+from pp16_softmax_model import pp16_row, wide_rows
 
 N = 16384
 D = 128
@@ -50,7 +50,16 @@ def built_margin() -> float:
     return float(m.group(1))
 
 
-def _worst(q, k, v, causal: bool, margin: float, rows=ROWS) -> tuple[float, list[dict]]:
+def built_spread() -> float:
+    from fa import native
+
+    m = re.search(r"pp16_spread=(\d+)", native.version())
+    assert m, native.version()
+    return float(m.group(1))
+
+
+def _worst(q, k, v, causal: bool, margin: float, rows=ROWS,
+           checked_from_start: bool = False) -> tuple[float, list[dict]]:
     """Largest |model - oracle| / (ATOL + RTOL |oracle|) over `rows` of head 0, and the infos."""
     n, d = q.shape[2], q.shape[3]
     c = np.float32(d ** -0.5 * math.log2(math.e))
@@ -60,7 +69,8 @@ def _worst(q, k, v, causal: bool, margin: float, rows=ROWS) -> tuple[float, list
     v32 = v[0, 0].float().numpy()
     worst, infos = 0.0, []
     for i, r in enumerate(rows):
-        out, info = pp16_row(s[i], v32, r, n, causal=causal, margin=margin)
+        out, info = pp16_row(s[i], v32, r, n, causal=causal, margin=margin,
+                             checked_from_start=checked_from_start)
         worst = max(worst, float((np.abs(out - ref[i]) / (ATOL + RTOL * np.abs(ref[i]))).max()))
         infos.append(info)
     return worst, infos
@@ -117,3 +127,57 @@ def test_model_second_pass_on_overflow():
         worst, infos = _worst(q, k, v, causal, built_margin(), rows)
         assert worst <= 1.0, (causal, worst)
         assert any(i["second_pass"] for i in infos)
+
+
+def _first_tiles(d: int, bc: int, std: float, seed: int, sink: float = 0.0,
+                 outliers: int = 0, chunks: int = 64, rows: int = 1024) -> np.ndarray:
+    """First key tiles' scores (times scale*log2(e)) of `chunks` items of `rows` query rows each:
+    q, k ~ N(0, std^2) in fp16; `sink` nats added to key 0's score; `outliers` keys of each
+    tile (at random positions) scaled x8."""
+    g = torch.Generator().manual_seed(seed)
+    c = d ** -0.5 * math.log2(math.e)
+    out = []
+    for _ in range(chunks):
+        q = (torch.randn(rows, d, generator=g) * std).half().float()
+        k = torch.randn(bc, d, generator=g) * std
+        if outliers:
+            k[torch.randperm(bc, generator=g)[:outliers]] *= 8.0
+        s = q @ k.half().float().t() * c
+        s[:, 0] += sink * math.log2(math.e)
+        out.append(s.numpy())
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("d, bc", [(128, 32), (64, 64)])
+def test_spread_vote_separates_input_classes(d, bc):
+    """The ping-pong's first-tile vote (softmax16_wide, restated by `wide_rows`) at the built
+    threshold, on 2^16 query rows per class: q, k ~ N(0, 1) (the BASELINE configs' inputs), the
+    same with an attention sink of 13 nats or with one or two keys x8 in the tile, leave every
+    row unflagged, so those items keep the unchecked tiles; q, k ~ N(0, 1.6^2) flags over a
+    tenth of the rows, so every 256-row item runs checked. Taking the largest lane range instead
+    of the smallest would flag the sink and outlier rows; a threshold near the benchmark rows'
+    largest range (about 7 exp2 units) would flag benchmark items. The layout (which lanes
+    hold which keys) is pinned in tests/test_geometry.py."""
+    spread = built_spread()
+    assert spread > 0
+    for name, kw in [("N(0,1)", {}), ("sink", {"sink": 13.0}), ("one outlier", {"outliers": 1}),
+                     ("two outliers", {"outliers": 2})]:
+        s = _first_tiles(d, bc, 1.0, seed=5, **kw)
+        assert not wide_rows(s, spread).any(), name
+        # margin below the threshold on the benchmark rows
+        assert not wide_rows(s, spread - 1.0).any() or name != "N(0,1)", name
+    wide = wide_rows(_first_tiles(d, bc, 1.6, seed=6), spread)
+    assert wide.mean() > 0.1, wide.mean()
+    assert wide.reshape(-1, 256).any(axis=1).all()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_wide_items_run_checked_from_the_start(causal):
+    """q, k ~ N(0, 1.6^2) at 16k keys: rows of an item that voted wide run every steady tile
+    checked (no second pass) and match the fp64 oracle at the north-star tolerance."""
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(1, 1, N, D, generator=g) * sc for sc in (1.6, 1.6, 1.0))
+    q, k, v = q.half(), k.half(), v.half()
+    worst, infos = _worst(q, k, v, causal, built_margin(), checked_from_start=True)
+    assert worst <= 1.0, worst
+    assert not any(i["second_pass"] for i in infos)
