@@ -5,7 +5,9 @@ length, head dim, causal, variant and softmax scale, with B*H*N small enough for
 spread so that every tile row (small grid key split, simple, ping-pong) and both
 sides of the size thresholds come up. Each case checks fa.forward_variant against the fp32
 oracle on two (b, h) slices with the north-star tolerance, and fa.forward_lse's LSE against the
-oracle's LSE (2e-3 absolute).
+oracle's LSE (2e-3 absolute). Further seeded draws take the head split, and ping-pong shapes
+under the input classes that steer its softmax (wide spreads, outlier keys, a sink, scores
+that widen late).
 """
 
 from __future__ import annotations
@@ -127,3 +129,63 @@ def test_random_head_split_case(i, b, h, n, d, heads):
         ref = orc.attention_fp32(q[sl], k[sl], v[sl])
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
         torch.testing.assert_close(lse[sl], orc.lse_fp32(q[sl], k[sl], False), atol=2e-3, rtol=0)
+
+
+# Ping-pong shapes (d=128 large grids in both modes, d=64 one-round grids) for the input-class
+# draws below: (b, h, n, d, causal).
+PP_SHAPES = [(4, 16, 4096, 128, False), (2, 16, 5000, 128, False), (1, 16, 8193, 128, False),
+             (8, 8, 2049, 128, False), (4, 16, 4096, 128, True), (2, 16, 5000, 128, True),
+             (1, 16, 8193, 128, True), (4, 8, 3300, 128, True), (1, 16, 4096, 64, False),
+             (1, 4, 16384, 64, False), (1, 8, 8000, 64, False)]
+KINDS = ["spread 1.3", "spread 1.6", "spread 2.0", "outliers", "sink", "late"]
+
+
+def _class_cases(count=14, seed=20261203):
+    rnd = random.Random(seed)
+    cases = [(i,) + PP_SHAPES[i % len(PP_SHAPES)] + (KINDS[i % len(KINDS)],)
+             for i in range(len(PP_SHAPES))]
+    while len(cases) < count:
+        cases.append((len(cases),) + rnd.choice(PP_SHAPES) + (rnd.choice(KINDS),))
+    return cases
+
+
+def _class_inputs(b, h, n, d, kind, seed):
+    """q, k, v fp16 on the CPU: ~N(0, 1), then per kind: q and k x s ("spread s": the first
+    tile's vote runs the ping-pong items checked from the start); 1 % of the key rows x8
+    ("outliers": items overflow their unchecked run and are redone, later workgroups start
+    checked); key 0 about 13 nats above the rest ("sink": neither); keys from n/3 on x2.5
+    ("late": scores that widen after the first tile, which the vote cannot see: redone)."""
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(b, h, n, d, generator=g) for _ in range(3))
+    if kind.startswith("spread"):
+        s = float(kind.split()[1])
+        q, k = q * s, k * s
+    elif kind == "outliers":
+        k = k * ((torch.rand(b, h, n, 1, generator=g) < 0.01).float() * 7.0 + 1.0)
+    elif kind == "sink":
+        q[..., 0] = 4.0
+        k[:, :, 0, 0] = 13.0 * d ** 0.5 / 4.0
+    else:
+        k[:, :, n // 3:] *= 2.5
+    return q.half(), k.half(), v.half()
+
+
+@pytest.mark.parametrize("i,b,h,n,d,causal,kind", _class_cases())
+def test_random_input_class_case(i, b, h, n, d, causal, kind):
+    """Seeded ping-pong shapes under the input classes that steer its softmax (the first tile's
+    wide-spread vote, the redo of an overflowing item, the launch's switch to checked starts,
+    or none of them): fa.forward against the fp32 oracle on the first and last (b, h) slices."""
+    import fa
+    from fa import native
+
+    tile = native.tile_config(d, causal, "opt", n, b, h)
+    print(f"case class {i}: B={b} H={h} N={n} d={d} causal={causal} {kind} tile={tile}",
+          flush=True)
+    assert tile["schedule"] == "pingpong16", tile
+    q, k, v = _class_inputs(b, h, n, d, kind, seed=3000 + i)
+    out = fa.forward(q.cuda(), k.cuda(), v.cuda(), causal=causal).cpu()
+    assert torch.isfinite(out).all()
+    for bi, hi in {(0, 0), (b - 1, h - 1)}:
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
