@@ -61,18 +61,21 @@ static __device__ unsigned long long pp_overflow_record;
 
 // Timeline probe, a development build option (off in the library): with FA_PROBE 1 wave 0 of
 // every ping-pong workgroup writes the 100 MHz constant clock (s_memrealtime) at fixed points
-// of its items, and its CU and XCC ids, into probe_stamps[blockIdx.x * 16 + slot];
+// of its items, and its CU and XCC ids, into probe_stamps[blockIdx.x * 32 + slot];
 // fa_probe_clear / fa_probe_read (exported only by such a build) hand the array to the host
 // (dev/fa_dev --probe, summarized by dev/probe.py). Slots: 0 kernel entry; per item i (0, 1),
 // 1 + 5i its first pass starts, 2 + 5i the prologue's loads have landed (after its barrier),
 // 3 + 5i the steady tiles are done, 4 + 5i the last tile is done, 5 + 5i the O stores are
 // issued; 12 a second pass starts; 11 and 13 the shader clock's cycle count (s_memtime) at the
-// workgroup's entry and end; 14 HW_ID; 15 XCC_ID.
+// workgroup's entry and end; 14 HW_ID; 15 XCC_ID; and within item i's phases, 16 + 5i the
+// prologue's loads are issued, 17 + 5i they have landed (the wave's own wait, before the
+// barrier), 18 + 5i the first tile's S is computed, 19 + 5i the first steady tile is done,
+// 20 + 5i the item's final test has passed its barrier.
 #ifndef FA_PROBE
 #define FA_PROBE 0
 #endif
 #if FA_PROBE
-constexpr int kProbeSlots = 16;
+constexpr int kProbeSlots = 32;
 constexpr unsigned kProbeWorkgroups = 1U << 16;
 static __device__ unsigned long long probe_stamps[kProbeWorkgroups * kProbeSlots];
 #endif
@@ -971,9 +974,14 @@ using PP16ReadSched = std::conditional_t<
 #endif
 
 // Flags that the waves of a workgroup share in LDS, ordered by the workgroup's barriers. Relaxed
-// workgroup-scope atomics compile to ds_read / ds_write, which wait for LDS alone; volatile
-// accesses compile to flat instructions (a volatile access keeps its generic address), which
-// also count as vector-memory operations, so each waited for every K/V prefetch in flight.
+// workgroup-scope atomics compile to ds_read / ds_write; volatile accesses compile to flat
+// instructions (a volatile access keeps its generic address), which also count as
+// vector-memory operations. The compiler still puts an s_waitcnt vmcnt(0) before each of these
+// ds accesses (the K/V tiles arrive by buffer-to-LDS DMA, which that counter tracks, and it
+// cannot tell the flags from the DMA's destinations), so a chunk-boundary test drains the K/V
+// prefetches in flight. Inline ds_read_b32 / ds_write_b32 avoid that wait but measured 0.1-1.1 %
+// slower on five ping-pong shapes (the prefetches have mostly landed by a chunk boundary, and
+// the register assignment moved), so the atomics stay.
 __device__ __forceinline__ int flag_get(const int& f) {
     return __hip_atomic_load(&f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -1675,6 +1683,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
         }
     }
     const Frag16<T> fr(lane);
+    probe_stamp(wave, lane, 16 + 5 * probe_item);
 
     f32x4 oacc[G::DB][G::QB];
 #pragma unroll
@@ -1684,6 +1693,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     float l_run[G::QB] = {0.0F, 0.0F};
 
     wait_vmem();
+    probe_stamp(wave, lane, 17 + 5 * probe_item);
     if constexpr (ADAPT) {
         if (!checked_pass && wave == 0 && lane == 0) {
             pp_adapt = static_cast<unsigned>(record >> 32) == launch_id &&
@@ -1710,6 +1720,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
 #pragma unroll
         for (int qb = 0; qb < G::QB; ++qb) s[kb][qb] = f32x4{};
     if (n_act > 0) qk16<T>(kbuf(I0{}), fr, qf, s);
+    probe_stamp(wave, lane, 18 + 5 * probe_item);
 
     // Returns true when the workgroup left its unchecked run on an overflow (FAST only).
     auto steady = [&](auto group) -> bool {
@@ -1817,6 +1828,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             if (n_busy > 0) {
                 tile(0, I0{}, Exact{});
                 jj = 1;
+                probe_stamp(wave, lane, 19 + 5 * probe_item);
             }
             // Unchecked tiles in steps of three, in chunks of 1, 2, 4, ... steps, at most
             // FA_PP16_EXIT_STEPS (an overflow tends to come early, as the running max of the
@@ -1943,6 +1955,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             const bool bad = !(l_run[0] < INFINITY && l_run[1] < INFINITY);
             if (wave_any(bad) && lane == 0) flag_set(pp_flags[2], 1);
             __syncthreads();
+            probe_stamp(wave, lane, 20 + 5 * probe_item);
             if (__builtin_amdgcn_readfirstlane(flag_get(pp_flags[2])) != 0) {
                 if constexpr (ADAPT) {
                     if (wave == 0 && lane == 0) note_overflow(launch_id);

@@ -18,7 +18,7 @@
 //   --probe PATH            (a library built with FA_PROBE=1, e.g. dev/ab.py build probe
 //                           --define FA_PROBE=1) after the timed launches, one more launch
 //                           with the ping-pong's timeline stamps cleared before it; writes
-//                           them to PATH (16 uint64 per workgroup; dev/probe.py reads them)
+//                           them to PATH (32 uint64 per workgroup; dev/probe.py reads them)
 //
 // Loads the kernel library at run time (dlopen) and calls only its C ABI (include/fa_hip.h),
 // as any foreign caller would: that lets the tuning sweep (dev/tune.py) time libraries built
@@ -384,8 +384,9 @@ int run(const Options& o) {
     if (!ok) std::printf("FAILED: |err| above 2e-3 + 1e-2 |ref| on a sampled row\n");
 
     if (!o.probe.empty()) {
-        // The stamps of one more launch (workgroups [0, 65536), 16 slots each), written up to
-        // the last workgroup that stamped.
+        // The stamps of one more launch (workgroups [0, 65536), kProbeSlots each), written up
+        // to the last workgroup that stamped.
+        constexpr size_t kProbeSlots = 32;
         void* h = dlopen(o.lib.c_str(), RTLD_NOW | RTLD_LOCAL | RTLD_NOLOAD);
         auto* clear = h ? reinterpret_cast<int (*)()>(dlsym(h, "fa_probe_clear")) : nullptr;
         auto* read = h ? reinterpret_cast<int (*)(void*, uint64_t)>(dlsym(h, "fa_probe_read"))
@@ -397,19 +398,20 @@ int run(const Options& o) {
         if (clear() != 0) throw std::runtime_error("fa_probe_clear failed");
         launch();
         hip_check(hipStreamSynchronize(stream), "probe launch");
-        std::vector<uint64_t> stamps(size_t{1} << 20);
+        std::vector<uint64_t> stamps((size_t{1} << 16) * kProbeSlots);
         if (read(stamps.data(), stamps.size() * sizeof(uint64_t)) != 0) {
             throw std::runtime_error("fa_probe_read failed");
         }
         size_t used = 0;
         for (size_t i = 0; i < stamps.size(); ++i) {
-            if (stamps[i] != 0) used = i / 16 + 1;
+            if (stamps[i] != 0) used = i / kProbeSlots + 1;
         }
         FILE* f = std::fopen(o.probe.c_str(), "wb");
         if (f == nullptr) throw std::runtime_error("cannot write " + o.probe);
-        const size_t wrote = std::fwrite(stamps.data(), sizeof(uint64_t), used * 16, f);
+        const size_t wrote =
+            std::fwrite(stamps.data(), sizeof(uint64_t), used * kProbeSlots, f);
         std::fclose(f);
-        if (wrote != used * 16) throw std::runtime_error("short write to " + o.probe);
+        if (wrote != used * kProbeSlots) throw std::runtime_error("short write to " + o.probe);
         std::printf("probe: %zu workgroups -> %s\n", used, o.probe.c_str());
     }
 

@@ -2,13 +2,16 @@
 
     python3 flash-attention-from-scratch_amd/dev/probe.py PATH [--json]
 
-Per workgroup the dump holds 16 uint64 values: the 100 MHz constant clock (s_memrealtime) at
+Per workgroup the dump holds 32 uint64 values: the 100 MHz constant clock (s_memrealtime) at
 slot 0 (kernel entry) and, for item i of the workgroup (0, or 1 for the second item of a causal
 pair), slots 1 + 5i .. 5 + 5i (its first pass starts, its prologue's loads have landed, its
 steady tiles are done, its last tile is done, its O stores are issued); slot 12 when a second
 pass starts; slots 11 and 13 the shader clock's cycle count (s_memtime) at the workgroup's
-entry and end; the HW_ID (14) and XCC_ID (15) hardware registers. Printed: medians over the
-workgroups of each phase of each item and of the gap between a pair's items; the idle time
+entry and end; the HW_ID (14) and XCC_ID (15) hardware registers; and slots 16 + 5i .. 20 + 5i
+inside item i's phases (its prologue's loads are issued, they have landed before the barrier,
+the first tile's S is computed, the first steady tile is done, the final test has passed its
+barrier). Printed: medians over the workgroups of each phase of each item, of the steps inside
+them (`detail`, when those stamps are present), and of the gap between a pair's items; the idle time
 between one workgroup's last stamp and the next workgroup's entry on the same CU; when the
 CUs and the XCDs finish, from the first workgroup's entry; and each XCD's median clock (cycles
 over 100 MHz ticks from entry to the last O store). Only the stamps of wave 0 are
@@ -24,13 +27,17 @@ from pathlib import Path
 
 import numpy as np
 
-SLOTS = 16
+SLOTS = 32
 TICKS_PER_US = 100.0  # s_memrealtime counts at 100 MHz
 PHASES = ("prologue", "steady", "last_tile", "final_and_store")
+# Steps inside an item, as (name, from slot, to slot) for item 0 (item 1: + 5 on every slot).
+DETAIL = (("issue_loads", 1, 16), ("load_wait", 16, 17), ("barrier_wait", 17, 2),
+          ("first_s", 2, 18), ("first_tile", 18, 19), ("steady_rest", 19, 3),
+          ("last_tile", 3, 4), ("final_test", 4, 20), ("store_issue", 20, 5))
 
 
 def load(path: Path) -> np.ndarray:
-    """The stamps as an int64 array [workgroups, 16] (workgroups that stamped nothing dropped)."""
+    """The stamps as an int64 array [workgroups, 32] (workgroups that stamped nothing dropped)."""
     raw = np.fromfile(path, dtype=np.uint64)
     if raw.size % SLOTS:
         raise ValueError(f"{path}: {raw.size} values, not a multiple of {SLOTS}")
@@ -62,6 +69,12 @@ def summarize(a: np.ndarray) -> dict:
         t = [us(a[have, base + k]) for k in range(5)]
         out["items"][i] = {name: float(np.median(t[k + 1] - t[k]))
                            for k, name in enumerate(PHASES)}
+        full = have & np.all(a[:, [lo + 5 * i for _, lo, _ in DETAIL]
+                               + [hi + 5 * i for _, _, hi in DETAIL]] != 0, axis=1)
+        if full.any():
+            out.setdefault("detail", {})[i] = {
+                name: float(np.median(us(a[full, hi + 5 * i]) - us(a[full, lo + 5 * i])))
+                for name, lo, hi in DETAIL}
         ends[have] = np.maximum(ends[have], t[4])
     out["entry_to_item"] = float(np.median(us(a[:, 1]) - us(a[:, 0])))
     if pairs:
@@ -101,6 +114,9 @@ def report(s: dict) -> str:
              f"entry to first item: {s['entry_to_item']:.2f} us"]
     for i, ph in s["items"].items():
         lines.append(f"item {i}: " + ", ".join(f"{k} {v:.2f} us" for k, v in ph.items()))
+        if i in s.get("detail", {}):
+            lines.append("  steps: " + ", ".join(f"{k} {v:.2f}" for k, v in
+                                                  s["detail"][i].items()) + " us")
     if s["pairs"]:
         lines.append(f"between a pair's items: {s['gap_between_items']:.2f} us")
     if s["gap_between_workgroups_on_a_cu"] is not None:

@@ -126,10 +126,10 @@ def test_fa_dev_runs_and_checks(args):
 
 def _stamps(wgs):
     """A synthetic timeline dump: per workgroup (cu, xcc, entry, [item phase lengths in
-    ticks]) -> 16 uint64 slots as the FA_PROBE build writes them."""
+    ticks]) -> 32 uint64 slots as the FA_PROBE build writes them (the phase stamps only)."""
     import numpy as np
 
-    out = np.zeros((len(wgs), 16), dtype=np.uint64)
+    out = np.zeros((len(wgs), 32), dtype=np.uint64)
     for w, (cu, xcc, entry, items) in enumerate(wgs):
         out[w, 0] = entry
         t = entry
@@ -213,3 +213,32 @@ def test_probe_xcd_clocks(tmp_path):
     s = probe.summarize(probe.load(path))
     assert s["xcd_clock_ghz"] == pytest.approx([2.0, 1.9])
     assert "GHz" in probe.report(s)
+
+
+def test_probe_summary_of_item_steps(tmp_path):
+    """The steps inside an item (slots 16-20): load issue 40 ticks, load wait 110, barrier wait
+    60 (the prologue's 210 ticks split), first S 70, first tile 130, the rest of the steady
+    tiles 9800 (the 10000 ticks of the steady phase split), last tile 100, final test 40 and
+    O-store issue 110 (the 150 ticks of the final phase split)."""
+    sys.path.insert(0, str(DEV))
+    import probe
+
+    a = _stamps([(0, 0, 1000, [(10, 210, 10000, 100, 150)])])
+    start = 1010
+    a[0, 16] = start + 40
+    a[0, 17] = start + 150
+    a[0, 18] = start + 210 + 70
+    a[0, 19] = start + 210 + 200
+    a[0, 20] = start + 210 + 10000 + 100 + 40
+    path = tmp_path / "steps.bin"
+    a.tofile(path)
+    s = probe.summarize(probe.load(path))
+    assert s["detail"][0] == pytest.approx({
+        "issue_loads": 0.4, "load_wait": 1.1, "barrier_wait": 0.6, "first_s": 0.7,
+        "first_tile": 1.3, "steady_rest": 98.0, "last_tile": 1.0, "final_test": 0.4,
+        "store_issue": 1.1})
+    assert "steps:" in probe.report(s)
+    # a dump without the step stamps has no detail
+    b = _stamps([(0, 0, 1000, [(10, 210, 10000, 100, 150)])])
+    b.tofile(path)
+    assert "detail" not in probe.summarize(probe.load(path))
