@@ -22,6 +22,8 @@ checks: no read shares a phase with a write to its slot; all eight waves read th
 and so leave at the same boundary, i.e. after the same number of barriers (group 0 then adds
 its one closing barrier, as after a full run); and a wave that overflows by step b makes the
 workgroup leave at the second boundary from b on (the one after the boundary that sees it).
+The first tile's wide-spread vote (pp_flags[3]) is checked the same way at the end: every wave
+reads it after every write, so all of them run the item checked or none does.
 """
 
 from __future__ import annotations
@@ -130,3 +132,50 @@ def test_model_catches_a_broken_protocol(mistake):
     with pytest.raises(AssertionError):
         for bad_at in _patterns(12, 200, seed=1):
             simulate(12, 2, bad_at, **kwargs)
+
+
+# ---- the first tile's wide-spread vote (pp_flags[3], FA_PP16_SPREAD) ---------------------------
+# A wave that finds a wide row in its item's first steady tile (tile 0, exact) sets the flag in
+# that tile's softmax phase S_0 (phase 1 + g); the flag was cleared before the prologue's
+# barrier (phase 0). Every wave that ran tile 0 reads it once tile 0 returns, i.e. in the phase of
+# its S_1 (3 + g), and runs the item checked if it is set. Waves without an active first tile
+# (a causal wave whose rows all precede its first keys) neither vote nor read: their unchecked
+# run is empty anyway.
+
+
+def vote_decisions(voters, read_phase) -> list:
+    """Each reading wave's decision for the set of voting waves; asserts that no read shares a
+    phase with a write (a race)."""
+    writes = [1 + _group(w) for w in voters]
+    out = []
+    for w in range(WAVES):
+        ph = read_phase(_group(w))
+        assert ph not in writes, ("read and write of the vote in one phase", w, ph)
+        out.append(any(p < ph for p in writes))
+    return out
+
+
+def _subsets():
+    for mask in range(1 << WAVES):
+        yield {w for w in range(WAVES) if mask >> w & 1}
+
+
+def test_spread_vote_is_read_alike_by_every_wave():
+    """All 256 sets of voting waves: every wave reads after every write (no race), so all eight
+    take the same decision, and it is 'checked' exactly when some wave voted."""
+    assert boundary_phase(0, 0) - 2 == 1 and boundary_phase(1, 0) - 2 == 2  # S_0 of each group
+    for voters in _subsets():
+        d = vote_decisions(voters, lambda g: boundary_phase(g, 0))  # the phase of S_1
+        assert len(set(d)) == 1 and d[0] == bool(voters), (voters, d)
+
+
+@pytest.mark.parametrize("mistake", ["read in the voting phase", "read in the first matrix phase"])
+def test_vote_model_catches_an_early_read(mistake):
+    """Reading the vote in S_0 itself, or in M_0 (the phase of group 1's S_0), races with a
+    write: both planted mistakes must be caught."""
+    read = {"read in the voting phase": lambda g: 1 + g,
+            "read in the first matrix phase": lambda g: 2 + g}[mistake]
+    with pytest.raises(AssertionError):
+        for voters in _subsets():
+            d = vote_decisions(voters, read)
+            assert len(set(d)) == 1
