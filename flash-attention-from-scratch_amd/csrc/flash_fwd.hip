@@ -1855,7 +1855,8 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
             // must mask (keys 0..q0 are visible to every row), i.e. the diagonal band. The
             // second pass runs every steady tile checked.
             // A wide-spread vote of the first tile (written in its softmax phase, read here after
-            // the barrier that ends both groups' first softmax phases) also runs the item checked.
+            // the barrier that ends both groups' first softmax phases, so every wave sees every
+            // vote: tests/test_abort_protocol.py) also runs the item checked.
             const bool wide = FA_PP16_SPREAD > 0 && jj == 1 && !checked_pass && !start_checked &&
                               __builtin_amdgcn_readfirstlane(flag_get(pp_flags[3])) != 0;
             const int n_free =
