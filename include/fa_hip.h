@@ -163,7 +163,7 @@ typedef struct fa_tile_info {
 int fa_tile_config(const fa_params* params, fa_tile_info* out);
 
 /* Library version string and softmax build options, e.g.
- * "fa_hip 0.2.0 gfx950 pp16_unchecked=1 pp16_margin=0". */
+ * "fa_hip 0.2.0 gfx950 pp16_unchecked=1 pp16_margin=0 pp16_spread=9". */
 const char* fa_version(void);
 
 #ifdef __cplusplus
