@@ -249,12 +249,26 @@ constexpr Work work_of(int block_id, int bh_count, int n_qblocks, bool causal) {
 // whatever B*H is; all items are equal, so the XCDs stay balanced. (work_of walks the heads with
 // consecutive ids, which scatters a head's query blocks in time: on many short heads, e.g.
 // 512 heads of 2048 keys, their K/V are then re-read from HBM by every query block.)
-// Causal grids keep work_of's global longest-first order: measured on MI355X, its tail (the
-// shortest query blocks last, everywhere at once) is worth more than the L2 locality, which
-// head-grouped orders buy only by mixing long and short blocks late in the launch.
+// Causal grids keep work_of's global longest-first order (its tail, the shortest query blocks
+// last everywhere at once, is worth more than L2 locality on most shapes), unless group_heads
+// > 0 (the launcher's choice, causal_group_heads): then the heads run in groups of group_heads,
+// longest query blocks first within each group, so that the query blocks of a head run close in
+// time and share its K/V in L2 and the last-level cache. With group_heads a multiple of 8 the
+// blocks of a head also stay on one XCD (id % 8 = head % 8 within a group).
 constexpr int kXcds = 8;
-constexpr Work work_of_xcd(int block_id, int bh_count, int n_qblocks, bool causal) {
-    if (causal) return work_of(block_id, bh_count, n_qblocks, causal);
+constexpr Work work_of_xcd(int block_id, int bh_count, int n_qblocks, bool causal,
+                           int group_heads = 0) {
+    if (causal) {
+        const int G = group_heads;
+        if (G > 0 && bh_count > G) {
+            const int grp = block_id / (G * n_qblocks);
+            const int first = grp * G;
+            const int heads = bh_count - first < G ? bh_count - first : G;  // last group: rest
+            const int r = block_id - grp * G * n_qblocks;
+            return Work{first + r % heads, n_qblocks - 1 - r / heads};
+        }
+        return work_of(block_id, bh_count, n_qblocks, causal);
+    }
     const int x = block_id % kXcds;
     const int slot = block_id / kXcds;
     const long long total = static_cast<long long>(bh_count) * n_qblocks;
@@ -366,6 +380,27 @@ inline bool causal_pairs_pay(long long bh_count, int n_qblocks, int slots) {
     const long long pairs = (w + slots - 1) / slots * (n_qblocks + 1);
     const long long singles = causal_singles_makespan(bh_count, n_qblocks, slots);
     return singles < 0 || 100 * pairs <= 103 * singles;
+}
+
+// Head groups of a causal simple-schedule grid (work_of_xcd's group_heads): 64 at head dim 128
+// from 256 heads on (four groups or more), else 0. At d = 128 the global longest-first order
+// re-reads a head's K/V from HBM for each of its query blocks, which run far apart in time.
+// Measured on MI355X (interleaved A/B, causal, the simple and 16x16x32 simple tiles):
+// 32x16x512 +16.6 %, 32x16x1024 +15 %, 16x16x1024 +7.7 %, 16x16x2048 +9.4 %, 21x16x768 +5.1 %.
+// With fewer groups the last one leaves CUs idle (10x16x1536, 2.5 groups: -7.8 %; 5x16x3072,
+// 1.25: -14 %), and at d = 64 the gains and losses were mixed (-6 to +7 % across shapes), so
+// those keep the global order. Host-side (launch argument). Build option
+// FA_CAUSAL_GROUP_HEADS: the group size (a multiple of 8), 0 for the global order everywhere.
+#ifndef FA_CAUSAL_GROUP_HEADS
+#define FA_CAUSAL_GROUP_HEADS 64
+#endif
+constexpr int kCausalGroupHeads = FA_CAUSAL_GROUP_HEADS;
+static_assert(kCausalGroupHeads >= 0 && kCausalGroupHeads % 8 == 0,
+              "head groups are whole multiples of the 8 XCDs");
+inline int causal_group_heads(int head_dim, long long bh_count) {
+    return kCausalGroupHeads > 0 && head_dim == 128 && bh_count >= 4LL * kCausalGroupHeads
+               ? kCausalGroupHeads
+               : 0;
 }
 
 }  // namespace fa::geom

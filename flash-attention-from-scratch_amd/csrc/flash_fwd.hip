@@ -471,7 +471,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
-    float* __restrict__ lse_part, unsigned /*launch_id*/) {
+    float* __restrict__ lse_part, unsigned /*launch_id*/, int group_heads) {
     // One LDS object per buffer, and the buffer of each tile fixed at compile time (the loop is
     // unrolled by the buffer count): the compiler then sees that the refill of one buffer cannot
     // alias the reads of another and waits for a tile's DMA only at the barrier that starts the
@@ -602,7 +602,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_kernel(
     // the dispatch gaps that the pairs remove.)
     run_item(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
                                 n_qblocks, CAUSAL)
-                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
+                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL, group_heads));
 }
 
 // Split-KV combine: for each row, LSE = log2-sum-exp2 of the splits' base-2 LSEs, and
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int /*tiles_per_split*/, float* /*o_part*/,
-    float* /*lse_part*/, unsigned /*launch_id*/) {
+    float* /*lse_part*/, unsigned /*launch_id*/, int group_heads) {
     constexpr int KS = T::KS;
     static_assert(KS == 2 || KS == 4, "two or four key parts");
     // One LDS object per (key part, buffer) for K and V, and the buffer of each step fixed at
@@ -691,7 +691,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_ksplit(
     const int wave = wave_uniform(threadIdx.x >> 6);
     const int part = wave / T::NW;  // key tiles part, part + KS, ...
     const int wq = wave % T::NW;    // which 32 query rows
-    const g::Work w = g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL);
+    const g::Work w = g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL, group_heads);
     const size_t head = static_cast<size_t>(w.bh) * n * T::D;
     const f16* kh = k + head;
     const f16* vh = v + head;
@@ -1563,7 +1563,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_pingpong16(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
-    float* __restrict__ lse_part, unsigned launch_id) {
+    float* __restrict__ lse_part, unsigned launch_id, int /*group_heads*/) {
     static_assert((T::D == 128 && T::BC == 32) || (T::D == 64 && T::BC == 64),
                   "the 16x16x32 layouts are written for D=128, BC=32 and D=64, BC=64");
     using G = M16<T>;
@@ -2192,7 +2192,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ o, float* __restrict__ lse, int n, int bh_count, int n_qblocks,
     float scale_log2, int negate_q, int tiles_per_split, float* __restrict__ o_part,
-    float* __restrict__ lse_part, unsigned /*launch_id*/) {
+    float* __restrict__ lse_part, unsigned /*launch_id*/, int group_heads) {
     static_assert(T::SCHED == SIMPLE16, "16x16x32 simple schedule");
     static_assert((T::D == 128 && T::BC == 32) || (T::D == 64 && T::BC == 64),
                   "the 16x16x32 layouts are written for D=128, BC=32 and D=64, BC=64");
@@ -2322,7 +2322,7 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
     };
     run_item(SPLIT ? g::work_of(static_cast<int>(blockIdx.x) - split * items, bh_count,
                                 n_qblocks, CAUSAL)
-                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL));
+                   : g::work_of_xcd(blockIdx.x, bh_count, n_qblocks, CAUSAL, group_heads));
 }
 
 // ---- tile table -------------------------------------------------------------------------------
@@ -2592,8 +2592,13 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
     float scale_log2 = sc.log2e_scaled;
     int negate_q = sc.negate_q;
     unsigned launch_id = next_launch_id();
+    // head groups of a causal simple-schedule grid (the ping-pong's causal grids run pairs or
+    // single blocks of their own order, the key split is for small grids)
+    int group_heads = CAUSAL && !SPLIT && (T::SCHED == SIMPLE || T::SCHED == SIMPLE16)
+                          ? g::causal_group_heads(T::D, bh)
+                          : 0;
     void* args[] = {&qp, &kp, &vp, &op, &lse, &n, &bh, &nqb, &scale_log2, &negate_q,
-                    &tiles_per_split, &o_part, &lse_part, &launch_id};
+                    &tiles_per_split, &o_part, &lse_part, &launch_id, &group_heads};
     dim3 grid(static_cast<unsigned>(n_qblocks) * static_cast<unsigned>(bh) *
               static_cast<unsigned>(n_splits));
     const void* fn;

@@ -61,6 +61,15 @@ void geom_work_of_xcd(int block_id, int bh_count, int n_qblocks, int causal, int
     *bh = w.bh;
     *qb = w.qb;
 }
+void geom_work_of_xcd_grouped(int block_id, int bh_count, int n_qblocks, int group_heads,
+                              int* bh, int* qb) {
+    const g::Work w = g::work_of_xcd(block_id, bh_count, n_qblocks, true, group_heads);
+    *bh = w.bh;
+    *qb = w.qb;
+}
+int geom_causal_group_heads(int head_dim, long long bh_count) {
+    return g::causal_group_heads(head_dim, bh_count);
+}
 long long geom_causal_singles_makespan(long long bh_count, int n_qblocks, int slots) {
     return g::causal_singles_makespan(bh_count, n_qblocks, slots);
 }

@@ -27,6 +27,8 @@ def geo():
     so = ctypes.CDLL(str(LIB))
     so.geom_work_of.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_work_of_xcd.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
+    so.geom_work_of_xcd_grouped.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_int)] * 2
+    so.geom_causal_group_heads.argtypes = [ctypes.c_int, ctypes.c_longlong]
     so.geom_split_range.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 2
     so.geom_causal_pair.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_int)] * 3
     so.geom_causal_pairs_pay.argtypes = [ctypes.c_longlong, ctypes.c_int, ctypes.c_int]
@@ -754,3 +756,44 @@ def test_mutants_leave_the_checks_green_on_the_real_layout(geo):
         test_m16_v_transposed_reads_are_conflict_free(same, d)
         test_v_transposed_reads_deliver_the_pv_keys(same, d)
         test_m16_v_transposed_reads_deliver_the_pv16_keys(same, d)
+
+
+def _grouped(geo, bid, bhc, nqb, group):
+    bh, qb = ctypes.c_int(), ctypes.c_int()
+    geo.geom_work_of_xcd_grouped(bid, bhc, nqb, group, ctypes.byref(bh), ctypes.byref(qb))
+    return bh.value, qb.value
+
+
+@pytest.mark.parametrize("bhc,nqb", [(256, 16), (336, 6), (512, 4), (300, 7), (64, 8), (65, 3)])
+def test_causal_head_groups(geo, bhc, nqb):
+    """work_of_xcd with head groups (causal simple-schedule grids at d=128 from 256 heads): a
+    bijection onto (head, query block); heads run in groups of 64 in order, longest query block
+    first within a group (the last group may be smaller); every query block of a head lands on
+    one XCD (id % 8); and 64 or fewer heads keep the global longest-first order."""
+    g = 64
+    items = [_grouped(geo, bid, bhc, nqb, g) for bid in range(bhc * nqb)]
+    assert sorted(items) == [(h, q) for h in range(bhc) for q in range(nqb)]
+    if bhc <= g:
+        assert items == [(bid % bhc, nqb - 1 - bid // bhc) for bid in range(bhc * nqb)]
+        return
+    pos = 0
+    for first in range(0, bhc, g):
+        heads = min(g, bhc - first)
+        chunk = items[pos:pos + heads * nqb]
+        assert {h for h, _ in chunk} == set(range(first, first + heads))
+        assert [q for _, q in chunk] == sorted((q for _, q in chunk), reverse=True)
+        pos += heads * nqb
+    xcd = {}
+    for bid, (h, _) in enumerate(items):
+        xcd.setdefault(h, set()).add(bid % 8)
+    if bhc % 8 == 0:
+        assert all(len(x) == 1 for x in xcd.values())
+
+
+def test_causal_group_heads_rule(geo):
+    """Head groups of 64 at head dim 128 from 256 heads (four groups) on, none at d=64 or with
+    fewer heads."""
+    assert geo.geom_causal_group_heads(128, 256) == 64
+    assert geo.geom_causal_group_heads(128, 512) == 64
+    assert geo.geom_causal_group_heads(128, 255) == 0
+    assert geo.geom_causal_group_heads(64, 1024) == 0

@@ -218,3 +218,38 @@ def test_simple16_rescale_paths(b, h, n, d, causal, kind):
         sl = (slice(bi, bi + 1), slice(hi, hi + 1))
         ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=causal)
         torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+
+
+# (B, H, N) causal d=128 grids of the simple schedules with 256 heads or more: the launcher runs
+# them in groups of 64 heads (fa::geom::causal_group_heads). 3x100x1500: four full groups and a
+# last one of 44 heads.
+GROUP_CASES = [(16, 16, 1024, "simple16"), (32, 16, 512, "simple"), (3, 100, 1500, "simple16"),
+               (2, 128, 2000, "simple16")]
+
+
+@pytest.mark.parametrize("b,h,n,sched", GROUP_CASES)
+def test_causal_head_groups(b, h, n, sched):
+    """fa.forward and fa.forward_lse on grouped causal grids against the oracle, on heads at
+    the edges of the groups (the first and last of the first two groups, the first of the last
+    group, the last head)."""
+    import fa
+    from fa import native
+
+    d = 128
+    tile = native.tile_config(d, True, "opt", n, b, h)
+    print(f"case groups B={b} H={h} N={n} tile={tile}", flush=True)
+    assert tile["schedule"] == sched
+    g = torch.Generator().manual_seed(n + h)
+    q, k, v = (torch.randn(b, h, n, d, generator=g).half() for _ in range(3))
+    out, lse = fa.forward_lse(q.cuda(), k.cuda(), v.cuda(), causal=True)
+    out, lse = out.cpu(), lse.cpu()
+    bh = b * h
+    o1 = fa.forward(q.cuda(), k.cuda(), v.cuda(), causal=True).cpu()
+    assert torch.equal(o1, out)
+    for f in sorted({0, 63, 64, 127, (bh - 1) // 64 * 64, bh - 1}):
+        bi, hi = divmod(f, h)
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        ref = orc.attention_fp32(q[sl], k[sl], v[sl], causal=True)
+        torch.testing.assert_close(out[sl].float(), ref, atol=ATOL, rtol=RTOL)
+        torch.testing.assert_close(lse[sl], orc.lse_fp32(q[sl], k[sl], causal=True), atol=2e-3,
+                                   rtol=0)
