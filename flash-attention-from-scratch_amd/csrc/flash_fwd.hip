@@ -2593,8 +2593,10 @@ int launch(const fa_params& p, float* lse, hipStream_t stream, Scale sc, int n_s
     int negate_q = sc.negate_q;
     unsigned launch_id = next_launch_id();
     // head groups of a causal simple-schedule grid (the ping-pong's causal grids run pairs or
-    // single blocks of their own order, the key split is for small grids)
-    int group_heads = CAUSAL && !SPLIT && (T::SCHED == SIMPLE || T::SCHED == SIMPLE16)
+    // single blocks of their own order, the key split is for small grids; the baseline variant
+    // keeps the first kernel's global order, as the yardstick the other variants are measured by)
+    int group_heads = CAUSAL && !SPLIT && (T::SCHED == SIMPLE || T::SCHED == SIMPLE16) &&
+                              p.variant != FA_VARIANT_BASELINE
                           ? g::causal_group_heads(T::D, bh)
                           : 0;
     void* args[] = {&qp, &kp, &vp, &op, &lse, &n, &bh, &nqb, &scale_log2, &negate_q,
