@@ -2433,6 +2433,13 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
 #ifndef FA_D128_CAUSAL_SHORT_MAX_N
 #define FA_D128_CAUSAL_SHORT_MAX_N 3072
 #endif
+// ... and up to this N where the grid runs in head groups (fa::geom::causal_group_heads: 256
+// heads or more), which make the 16x16x32 simple tile faster than the ping-pong there:
+// 16x16x3500 +5.5 %, 16x16x4096 +3.8 %, 8x32x4096 +3.5 % in interleaved A/B; even at 5000 and
+// 6144 (-0.6 to +0.1 %).
+#ifndef FA_D128_CAUSAL_GROUPED_MAX_N
+#define FA_D128_CAUSAL_GROUPED_MAX_N 4096
+#endif
 #ifndef FA_SMALL_GRID_WGS
 #define FA_SMALL_GRID_WGS 256
 #endif
@@ -2504,7 +2511,10 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
         return n <= FA_D128_SHORT_MAX_N ? OPT_D128_SHORT : OPT_D128;
     }
     if (n <= FA_D128_CAUSAL_VSHORT_MAX_N) return OPT_D128_C_VSHORT;
-    return n <= FA_D128_CAUSAL_SHORT_MAX_N ? OPT_D128_C_SHORT : OPT_D128_C;
+    if (n <= FA_D128_CAUSAL_SHORT_MAX_N) return OPT_D128_C_SHORT;
+    return n <= FA_D128_CAUSAL_GROUPED_MAX_N && g::causal_group_heads(128, bh) > 0
+               ? OPT_D128_C_SHORT
+               : OPT_D128_C;
 }
 
 // Calls f(Row<id>{}) with the row as a compile-time type.

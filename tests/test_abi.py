@@ -149,7 +149,13 @@ def test_tile_config_rows():
     assert _tile(128, True, "opt", 512) == simple128x4
     assert _tile(128, True, "opt", 513) == simple16_128x4
     assert _tile(128, True, "opt", 3072) == simple16_128x4
-    assert _tile(128, True, "opt", 3073) == pingpong128
+    # above 3072 keys the ping-pong, except grids that run in head groups (256 heads or more:
+    # fa::geom::causal_group_heads) up to 4096 keys
+    assert _tile(128, True, "opt", 3073, 4, 16) == pingpong128        # 64 heads
+    assert _tile(128, True, "opt", 4096, 8, 16) == pingpong128        # 128 heads
+    assert _tile(128, True, "opt", 3073) == simple16_128x4            # 512 heads
+    assert _tile(128, True, "opt", 4096, 16, 16) == simple16_128x4    # 256 heads
+    assert _tile(128, True, "opt", 4097) == pingpong128
     # fewer 8-wave workgroups than CUs: B*H*ceil(N/256) < 256 -> key-split tiles (64 rows,
     # two waves on each 32 rows)
     assert _tile(64, True, "opt", 900, 2, 8) == (64, 64, 4, 65536, "ksplit")

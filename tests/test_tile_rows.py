@@ -89,6 +89,8 @@ SWITCHES = [
     (4, 32, 1536, 128, False, S16_128X4), (4, 32, 1537, 128, False, PP128),
     (4, 32, 512, 128, True, SIMPLE128X4), (4, 32, 513, 128, True, S16_128X4),
     (1, 32, 3072, 128, True, S16_128X4), (1, 32, 3073, 128, True, PP128),
+    # grids in head groups (256 heads or more) keep the 16x16x32 simple tile up to 4096 keys
+    (8, 32, 4096, 128, True, S16_128X4), (8, 32, 4097, 128, True, PP128),
     (4, 16, 2048, 64, True, SIMPLE64X8), (4, 16, 2049, 64, True, S16_64X8),
     # d=64 ping-pong for one round of 256 items from 4096 keys
     (1, 16, 4095, 64, False, S16_64X8), (1, 16, 4096, 64, False, PP64),
