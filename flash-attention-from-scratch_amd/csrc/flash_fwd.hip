@@ -2403,6 +2403,22 @@ __global__ __launch_bounds__(T::THREADS) void flash_fwd_simple16(
 #ifndef FA_D64_CAUSAL_SHORT_MAX_N
 #define FA_D64_CAUSAL_SHORT_MAX_N 2048
 #endif
+// Causal d = 64 grids of at most FA_D64_CAUSAL_ROUND_MAX_WGS items (B*H*ceil(N/256); one round
+// of the 64-key tiles' two workgroups per CU) at N >= FA_D64_CAUSAL_ROUND_MIN_N: such a grid
+// lasts as long as its longest items, and 128-key tiles halve their tile steps (1x16x4096 +21 %,
+// 1x8x8192 +23 %, 2x16x4096 +12 %, 4x16x1536 +13 %, 4x16x2048 +5 %), although their 167 VGPRs
+// leave one workgroup per CU. On larger grids the longer tile's diagonal waste and the lost
+// second workgroup cost more than the steps save (5x16x2048 -6 %, 3x16x4096 -4 %), and at
+// N = 1024 it gains or loses with the grid's fill (+10 % to -2 %).
+#ifndef FA_OPT_D64_CAUSAL_ROUND
+#define FA_OPT_D64_CAUSAL_ROUND 128, 8, true, SIMPLE
+#endif
+#ifndef FA_D64_CAUSAL_ROUND_MIN_N
+#define FA_D64_CAUSAL_ROUND_MIN_N 1536
+#endif
+#ifndef FA_D64_CAUSAL_ROUND_MAX_WGS
+#define FA_D64_CAUSAL_ROUND_MAX_WGS 512
+#endif
 #ifndef FA_OPT_D128_VSHORT
 #define FA_OPT_D128_VSHORT 32, 4, true, SIMPLE
 #endif
@@ -2454,8 +2470,8 @@ enum TileId : int {
     BASE_D64, BASE_D64_C, BASE_D128, BASE_D128_C,
     OPT_D64_SMALL, OPT_D64_C_SMALL, OPT_D128_SMALL, OPT_D128_C_SMALL,
     OPT_D64_TINY, OPT_D64_C_TINY, OPT_D128_TINY, OPT_D128_C_TINY,
-    OPT_D64, OPT_D64_ONE_ROUND, OPT_D64_C_SHORT, OPT_D64_C, OPT_D128_VSHORT, OPT_D128_SHORT,
-    OPT_D128,
+    OPT_D64, OPT_D64_ONE_ROUND, OPT_D64_C_SHORT, OPT_D64_C, OPT_D64_C_ROUND, OPT_D128_VSHORT,
+    OPT_D128_SHORT, OPT_D128,
     OPT_D128_C_VSHORT, OPT_D128_C_SHORT, OPT_D128_C,
 };
 template <int ID> struct Row;
@@ -2475,6 +2491,7 @@ template <> struct Row<OPT_D64> : Entry<Tile<64, FA_OPT_D64>, false> {};
 template <> struct Row<OPT_D64_ONE_ROUND> : Entry<Tile<64, FA_OPT_D64_ONE_ROUND>, false> {};
 template <> struct Row<OPT_D64_C_SHORT> : Entry<Tile<64, FA_OPT_D64_CAUSAL_SHORT>, true> {};
 template <> struct Row<OPT_D64_C> : Entry<Tile<64, FA_OPT_D64_CAUSAL>, true> {};
+template <> struct Row<OPT_D64_C_ROUND> : Entry<Tile<64, FA_OPT_D64_CAUSAL_ROUND>, true> {};
 template <> struct Row<OPT_D128_VSHORT> : Entry<Tile<128, FA_OPT_D128_VSHORT>, false> {};
 template <> struct Row<OPT_D128_SHORT> : Entry<Tile<128, FA_OPT_D128_SHORT>, false> {};
 template <> struct Row<OPT_D128> : Entry<Tile<128, FA_OPT_D128>, false> {};
@@ -2504,6 +2521,9 @@ TileId tile_id(int head_dim, bool causal, int variant, int n, int64_t bh) {
             const int64_t items = bh * ((static_cast<int64_t>(n) + 255) / 256);
             return n >= FA_D64_ONE_ROUND_MIN_N && items <= g::kCus ? OPT_D64_ONE_ROUND : OPT_D64;
         }
+        if (n >= FA_D64_CAUSAL_ROUND_MIN_N &&
+            bh * ((static_cast<int64_t>(n) + 255) / 256) <= FA_D64_CAUSAL_ROUND_MAX_WGS)
+            return OPT_D64_C_ROUND;
         return n <= FA_D64_CAUSAL_SHORT_MAX_N ? OPT_D64_C_SHORT : OPT_D64_C;
     }
     if (!causal) {
@@ -2537,6 +2557,7 @@ decltype(auto) with_row(TileId id, F&& f) {
         case OPT_D64_ONE_ROUND: return f(Row<OPT_D64_ONE_ROUND>{});
         case OPT_D64_C_SHORT: return f(Row<OPT_D64_C_SHORT>{});
         case OPT_D64_C: return f(Row<OPT_D64_C>{});
+        case OPT_D64_C_ROUND: return f(Row<OPT_D64_C_ROUND>{});
         case OPT_D128_VSHORT: return f(Row<OPT_D128_VSHORT>{});
         case OPT_D128_SHORT: return f(Row<OPT_D128_SHORT>{});
         case OPT_D128: return f(Row<OPT_D128>{});

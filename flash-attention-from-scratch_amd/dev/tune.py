@@ -66,9 +66,14 @@ SLOTS = {
     "opt_d128_causal_tiny": ("FA_OPT_D128_TINY", "opt", 128, 1, _TINY),
     "opt_d64": ("FA_OPT_D64", "opt", 64, 0, [*_BIG, f"-DFA_D64_ONE_ROUND_MIN_N={_ALL}"]),
     "opt_d64_causal_short": ("FA_OPT_D64_CAUSAL_SHORT", "opt", 64, 1,
-                             [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_ALL}"]),
+                             [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_ALL}",
+                              f"-DFA_D64_CAUSAL_ROUND_MAX_WGS={_NONE}"]),
     "opt_d64_causal": ("FA_OPT_D64_CAUSAL", "opt", 64, 1,
-                       [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_NONE}"]),
+                       [*_BIG, f"-DFA_D64_CAUSAL_SHORT_MAX_N={_NONE}",
+                        f"-DFA_D64_CAUSAL_ROUND_MAX_WGS={_NONE}"]),
+    "opt_d64_causal_round": ("FA_OPT_D64_CAUSAL_ROUND", "opt", 64, 1,
+                             [*_BIG, f"-DFA_D64_CAUSAL_ROUND_MIN_N={_NONE}",
+                              f"-DFA_D64_CAUSAL_ROUND_MAX_WGS={_ALL}"]),
     "opt_d128_vshort": ("FA_OPT_D128_VSHORT", "opt", 128, 0,
                         [*_BIG, f"-DFA_D128_VSHORT_MAX_N={_ALL}"]),
     "opt_d128_short": ("FA_OPT_D128_SHORT", "opt", 128, 0,

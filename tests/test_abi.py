@@ -141,7 +141,13 @@ def test_tile_config_rows():
     assert _tile(64, False, "opt", 16384, 1, 4) == pingpong64
     assert _tile(64, False, "opt", 4000, 1, 16) == simple16_64x8
     assert _tile(64, False, "opt", 4096, 1, 17) == simple16_64x8
-    assert _tile(64, True, "opt", 4096, 1, 16) == simple16_64x8
+    # causal grids of at most 512 items from 1536 keys: 128-key simple tiles
+    round64 = (256, 128, 8, 65536, "simple")
+    assert _tile(64, True, "opt", 4096, 1, 16) == round64
+    assert _tile(64, True, "opt", 4096, 2, 16) == round64
+    assert _tile(64, True, "opt", 4096, 2, 17) == simple16_64x8
+    assert _tile(64, True, "opt", 1536, 4, 16) == round64
+    assert _tile(64, True, "opt", 1535, 4, 16) == simple64x8
     assert _tile(128, False, "opt", 256) == simple128x4
     assert _tile(128, False, "opt", 257) == simple16_128x4
     assert _tile(128, False, "opt", 1536) == simple16_128x4

@@ -24,11 +24,11 @@ def _tile(b, h, n, d, causal, variant="opt"):
 
 # Every (head_dim, causal, tile) the opt table can pick: the key split for small grids, the
 # simple schedule on 32x32x16 MFMAs (d=64 causal up to 2048 keys, d=128 up to 256 keys, causal
-# 512) or on 16x16x32 MFMAs, and the ping-pong (d=128 long sequences, d=64 non-causal grids of
+# 512; 128-key tiles for causal d=64 grids of at most 512 items) or on 16x16x32 MFMAs, and the ping-pong (d=128 long sequences, d=64 non-causal grids of
 # one round).
 OPT_ROWS = {
     (64, False, rows.SMALL64), (64, True, rows.SMALL64),
-    (64, True, rows.SIMPLE64X8),
+    (64, True, rows.SIMPLE64X8), (64, True, rows.ROUND64),
     (64, False, rows.S16_64X8), (64, True, rows.S16_64X8), (64, False, rows.PP64),
     (128, False, rows.SMALL128), (128, True, rows.SMALL128),
     (128, False, rows.SIMPLE128X4), (128, True, rows.SIMPLE128X4),

@@ -173,7 +173,8 @@ TAIL_SHAPES = [
     (1, 2, 450, 128, False, "opt"), (1, 2, 449, 128, True, "opt"),         # (four/two-way)
     (4, 16, 1001, 64, False, "opt"), (4, 16, 999, 64, True, "opt"),        # simple 8 waves
     (1, 32, 2501, 64, False, "opt"),                                        # (16x16x32 and
-    (1, 8, 8000, 64, False, "opt"), (1, 8, 8500, 64, True, "opt"),         # 32x32x16 MFMAs)
+    (1, 8, 8000, 64, False, "opt"), (2, 8, 8500, 64, True, "opt"),         # 32x32x16 MFMAs)
+    (3, 16, 1699, 64, True, "opt"),                                         # 128-key causal
     (8, 16, 703, 128, False, "opt"), (4, 16, 1003, 128, True, "opt"),      # simple 4 waves
     (16, 16, 251, 128, False, "opt"), (16, 16, 509, 128, True, "opt"),
     (2, 16, 2501, 128, False, "opt"), (1, 16, 4001, 128, True, "opt"),     # ping-pong d=128

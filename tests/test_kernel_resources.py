@@ -46,6 +46,8 @@ def _min_occupancy(name: str) -> int:
     if family == "flash_fwd_ksplit":
         return 2                      # two 4-wave workgroups (64 KiB) or one 8-wave (128 KiB)
     assert (family, sched) in (("flash_fwd_kernel", SIMPLE), ("flash_fwd_simple16", SIMPLE16)), name
+    if d == 64 and bc == 128:
+        return 2                      # one-round causal grids: one 8-wave workgroup per CU
     return 4 if d == 64 else 2        # d=64: two 8-wave workgroups per CU
 
 

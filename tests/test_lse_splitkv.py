@@ -42,7 +42,8 @@ LSE_CASES = [
     (1, 4, 1100, 64, True), (1, 2, 450, 128, False),      # (four-way d=64, two-way d=128)
     (4, 16, 1000, 64, True), (8, 16, 700, 128, False),    # simple 8 and 4 waves, large grid
     (16, 16, 250, 128, False),                            # (on 32x32x16 and 16x16x32 MFMAs)
-    (1, 16, 5000, 64, True), (2, 16, 2500, 128, False),   # simple d=64 long / ping-pong d=128
+    (2, 16, 5000, 64, True), (2, 16, 2500, 128, False),   # simple d=64 long / ping-pong d=128
+    (3, 16, 1700, 64, True),                              # 128-key tiles, causal d=64
     (1, 16, 4000, 128, True),                             # ping-pong causal
     (1, 8, 8000, 64, False),                              # ping-pong d=64, one round
 ]

@@ -45,6 +45,7 @@ def _check(b, h, n, d, causal, want, seed=11):
 PP128 = (256, 32, 8, 49152, "pingpong16")      # ping-pong, d=128
 PP64 = (256, 64, 8, 49152, "pingpong16")       # ping-pong, d=64 (one round of 256 items)
 SIMPLE64X8 = (256, 64, 8, 32768, "simple")     # 32x32x16 MFMAs
+ROUND64 = (256, 128, 8, 65536, "simple")       # causal d=64 grids of at most 512 items
 S16_64X8 = (256, 64, 8, 32768, "simple16")     # the simple schedule on 16x16x32 MFMAs
 SIMPLE128X4 = (128, 32, 4, 32768, "simple")
 S16_128X4 = (128, 32, 4, 32768, "simple16")
@@ -68,8 +69,9 @@ ROWS = [
     (1, 8, 8000, 64, False, PP64),            # 256 items: one round of one workgroup per CU
     (1, 9, 8000, 64, False, S16_64X8),
     (4, 16, 1000, 64, True, SIMPLE64X8),
-    (1, 32, 2500, 64, True, S16_64X8),
-    (1, 8, 8500, 64, True, S16_64X8),
+    (3, 32, 2500, 64, True, S16_64X8),
+    (2, 8, 8500, 64, True, S16_64X8),
+    (2, 16, 2000, 64, True, ROUND64),
     (16, 16, 250, 128, False, SIMPLE128X4),
     (8, 16, 700, 128, False, S16_128X4),
     (2, 16, 2500, 128, False, PP128),
@@ -91,13 +93,15 @@ SWITCHES = [
     (1, 32, 3072, 128, True, S16_128X4), (1, 32, 3073, 128, True, PP128),
     # grids in head groups (256 heads or more) keep the 16x16x32 simple tile up to 4096 keys
     (8, 32, 4096, 128, True, S16_128X4), (8, 32, 4097, 128, True, PP128),
-    (4, 16, 2048, 64, True, SIMPLE64X8), (4, 16, 2049, 64, True, S16_64X8),
+    (4, 16, 1535, 64, True, SIMPLE64X8), (4, 16, 1536, 64, True, ROUND64),
+    (2, 16, 4096, 64, True, ROUND64), (2, 17, 4096, 64, True, S16_64X8),
+    (8, 16, 2048, 64, True, SIMPLE64X8), (8, 16, 2049, 64, True, S16_64X8),
     # d=64 ping-pong for one round of 256 items from 4096 keys
     (1, 16, 4095, 64, False, S16_64X8), (1, 16, 4096, 64, False, PP64),
     (1, 17, 4096, 64, False, S16_64X8), (1, 4, 16384, 64, False, PP64),
     # small-grid boundary: B*H*ceil(N/256) = 255 and 256 workgroups of 8 waves
     (1, 17, 3840, 128, False, SMALL128), (1, 16, 4096, 128, False, PP128),
-    (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, S16_64X8),
+    (1, 17, 3840, 64, True, SMALL64), (1, 16, 4096, 64, True, ROUND64),
     # four-way split: at most 256 query blocks of 64 rows and at least 16 key tiles
     (1, 16, 1024, 64, False, TINY64), (1, 17, 1024, 64, False, SMALL64),
     (1, 16, 960, 64, True, SMALL64), (1, 16, 961, 64, True, TINY64),
@@ -152,7 +156,7 @@ def test_more_heads_than_the_reference_grid_limit(d, causal):
 PP_SCALE_CASES = [(4, 16, 1700, False), (2, 16, 3300, True)]
 # (B, H, N, d, causal, tile): the rows on 16x16x32 MFMAs
 M16_SCALE_CASES = [(b, h, n, 128, c, PP128) for b, h, n, c in PP_SCALE_CASES] + [
-    (4, 16, 1100, 64, False, S16_64X8), (2, 16, 3100, 64, True, S16_64X8),
+    (4, 16, 1100, 64, False, S16_64X8), (3, 16, 3100, 64, True, S16_64X8),
     (8, 16, 700, 128, False, S16_128X4), (4, 16, 1500, 128, True, S16_128X4),
 ]
 
