@@ -2744,6 +2744,8 @@ struct SplitPlan {
 // the row's TARGET_WGS (at least MIN_KEYS keys), so that about that many workgroups have work;
 // otherwise the longest query block's tiles are cut into `requested` ranges. Workspace: fp32 O
 // and LSE per split and row.
+bool causal_round_split(const fa_params& p);
+
 SplitPlan split_plan(const fa_params& p, int requested) {
     struct Consts {
         int br, bc, target_wgs, min_keys;
@@ -2760,6 +2762,8 @@ SplitPlan split_plan(const fa_params& p, int requested) {
     int tps;
     if (requested > 0) {
         tps = g::ceil_div(max_tiles, min(requested, max_tiles));
+    } else if (p.head_dim == 128 && causal_round_split(p)) {
+        tps = g::ceil_div(max_tiles, 2);  // one-round causal grids: two ranges
     } else {
         int64_t pairs = 0;
         for (int qb = 0; qb < nqb; ++qb) {
@@ -2791,8 +2795,34 @@ SplitPlan split_plan(const fa_params& p, int requested) {
 #ifndef FA_SPLITKV_MIN_N_D64_CAUSAL
 #define FA_SPLITKV_MIN_N_D64_CAUSAL 16384
 #endif
+// Causal grids of about one round of 256-row query blocks (FA_SMALL_GRID_WGS to
+// FA_SPLITKV_ROUND_MAX_WGS blocks) from FA_SPLITKV_ROUND_MIN_N keys: a single launch lasts as
+// long as its longest query block, which holds every key tile, while most CUs finish early.
+// Split-KV halves that block. Measured on MI355X with dev/fa_dev, single launch against the
+// split pair (interleaved, 3 rounds), d = 128 with two ranges: 1x8x8192 +11.4 to +12.6 %,
+// 1x4x16384 +22.1 %, 2x2x16384 +27.5 %, 1x2x32768 +31.8 %, 1x1x65536 +36.3 %, 1x6x12288 (288
+// blocks) +12.7 %, 1x9x8192 (288) +5.1 %; the automatic plan's 3-4 ranges gained less. d = 64
+// with the automatic plan: 1x8x8192 +12.5 %, 1x4x16384 +24.0 %, 1x2x32768 +29.9 %, 1x9x8192
+// +7.2 %. Past the bounds: 1x16x4096 -1.5 % (d = 128) and -1.3 % (d = 64); 320 blocks
+// (1x10x8192, 1x5x16384) +1.6 and +5.2 %; 512 blocks (1x16x8192 d = 128, 2x4x16384 d = 64)
+// -12 % and -15 %.
+#ifndef FA_SPLITKV_ROUND_MIN_N
+#define FA_SPLITKV_ROUND_MIN_N 8192
+#endif
+#ifndef FA_SPLITKV_ROUND_MAX_WGS
+#define FA_SPLITKV_ROUND_MAX_WGS 288
+#endif
+bool causal_round_split(const fa_params& p) {
+    if (p.variant == FA_VARIANT_BASELINE || !p.causal || p.seqlen < FA_SPLITKV_ROUND_MIN_N)
+        return false;
+    const int64_t blocks =
+        static_cast<int64_t>(p.batch) * p.heads * ((static_cast<int64_t>(p.seqlen) + 255) / 256);
+    return blocks >= FA_SMALL_GRID_WGS && blocks <= FA_SPLITKV_ROUND_MAX_WGS;
+}
+
 bool splitkv_preferred(const fa_params& p) {
     if (p.variant == FA_VARIANT_BASELINE || p.seqlen < FA_SPLITKV_MIN_N) return false;
+    if (causal_round_split(p)) return true;
     if (p.head_dim == 64 && p.causal && p.seqlen < FA_SPLITKV_MIN_N_D64_CAUSAL) return false;
     const int64_t bh = static_cast<int64_t>(p.batch) * p.heads;
     if (bh * ((static_cast<int64_t>(p.seqlen) + 255) / 256) >= FA_SMALL_GRID_WGS) return false;

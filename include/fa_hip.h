@@ -103,7 +103,9 @@ typedef struct fa_splitkv_info {
     int32_t preferred;        /* 1 if the automatic split-KV plan is expected to beat
                                  fa_flash_fwd on these params (variant not baseline, a grid
                                  that leaves most CUs idle, N >= 4096; causal at D = 64:
-                                 N >= 16384), else 0; independent of num_splits. The PyTorch
+                                 N >= 16384; or a causal grid of 256 to 288 query blocks of
+                                 256 rows, N >= 8192, where the automatic plan takes two
+                                 ranges at D = 128), else 0; independent of num_splits. The PyTorch
                                  binding's forward takes the split path exactly when it is 1. */
     int32_t reserved;         /* 0                                                            */
 } fa_splitkv_info;

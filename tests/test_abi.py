@@ -216,7 +216,8 @@ def test_lse_entry_rejects_bad_lse_pointer():
 
 
 @pytest.mark.parametrize("b,h,n,d,causal", [(1, 2, 16384, 128, False), (1, 2, 16384, 128, True),
-                                            (1, 2, 32768, 128, True),
+                                            (1, 2, 32768, 128, True), (1, 8, 8192, 128, True),
+                                            (1, 8, 8192, 64, True), (1, 4, 32768, 128, True),
                                             (2, 8, 1000, 64, True), (1, 1, 1, 64, False),
                                             (16, 32, 2048, 64, True)])
 def test_splitkv_plan(b, h, n, d, causal):
@@ -248,8 +249,10 @@ def test_splitkv_plan(b, h, n, d, causal):
         # causal, small grid: 2 heads x 4 x (1 + ... + 128) = 66048 (block, tile) pairs / 1024
         # target workgroups -> 65 tiles
         (1, 2, 16384, 128, True): 65,
-        # causal: 2 heads x 8 x (1 + ... + 128) = 132096 pairs / 512 -> 258 tiles
-        (1, 2, 32768, 128, True): 258,
+        # causal, one round of 256 query blocks from 8192 keys: two ranges of the 1024 tiles
+        (1, 2, 32768, 128, True): 512, (1, 8, 8192, 128, True): 128,
+        # causal: 4 heads x 8 x (1 + ... + 128) = 264192 pairs / 512 -> 516 tiles
+        (1, 4, 32768, 128, True): 516,
     }
     if (b, h, n, d, causal) in known:
         assert native.splitkv_plan(p, 0)["tiles_per_split"] == known[(b, h, n, d, causal)]
@@ -278,6 +281,14 @@ def test_splitkv_entry_rejects_bad_workspace():
     (1, 1, 16384, 128, False, "opt", 1), (1, 2, 16384, 128, True, "opt", 1),
     (1, 1, 32768, 128, True, "fp16acc", 1), (1, 2, 4096, 128, True, "opt", 1),
     (1, 4, 8192, 64, False, "opt", 1),
+    # causal grids of 256 to 288 query blocks of 256 rows from 8192 keys
+    (1, 8, 8192, 128, True, "opt", 1), (1, 9, 8192, 128, True, "opt", 1),
+    (1, 4, 16384, 64, True, "opt", 1), (1, 8, 8192, 64, True, "fp16acc", 1),
+    (1, 10, 8192, 128, True, "opt", 0),        # 320 blocks
+    (1, 16, 4096, 128, True, "opt", 0),        # N below 8192
+    (1, 8, 8191, 64, True, "opt", 0),
+    (1, 8, 8192, 128, False, "opt", 0),        # not causal
+    (1, 8, 8192, 128, True, "baseline", 0),
     # one step past each boundary of the rule
     (1, 2, 4095, 128, True, "opt", 0),         # N below 4096
     (1, 4, 8192, 64, True, "opt", 0),          # causal d = 64

@@ -72,6 +72,8 @@ ROUTED = [
     (1, 1, 32768, 128, False), (1, 1, 32768, 128, True),
     (1, 2, 4096, 128, True), (1, 4, 8192, 64, False),
     (1, 1, 16384, 64, True),     # causal d = 64 from 16384 keys
+    (1, 8, 8192, 128, True),     # causal, one round of 256 query blocks from 8192 keys
+    (1, 8, 8192, 64, True),
 ]
 
 
@@ -101,7 +103,9 @@ NOT_ROUTED = [
     # each is one step over a boundary of the routing rule
     (1, 2, 4095, 128, True),     # N below 4096
     (1, 4, 8192, 64, True),      # causal d = 64 below 16384 keys keeps the single launch
-    (1, 4, 16383, 64, True),
+    (1, 10, 8192, 128, True),    # causal, 320 query blocks: more than one round
+    (1, 16, 4096, 128, True),    # causal, one round below 8192 keys
+    (1, 3, 16383, 64, True),     # (a small grid)
     (1, 16, 4096, 128, False),   # 16 x 16 = 256 workgroups of 8 waves: fills the GPU
     (2, 8, 1000, 64, True),      # the benchmark's ragged config: short
 ]
